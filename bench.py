@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Benchmark of the InfLLM-v2 selection path on one MI355X.
+
+Metric: "stage1 TFLOP/s (% bf16 MFMA peak); maxpool+block-table
+GB/s (% HBM) @32K".  One step runs the three kernels on their "@32K" headline
+configurations with inputs resident in HBM:
+
+* stage 1   : cfg3, 4 x 8192-token causal prefill, Hq=32/Hkv=2/D=128, bf16 in,
+              fp32 scores [2, 32768, 512];
+* max-pool  : cfg2, 34816 rows of 1024 fp32 scores -> [2, 34816, 256];
+* block tab.: the block-table stage of cfg5 (4096 query tokens of a 131072-token
+              context, H=2, top-64) -> int32 [4096, 2, 4096] (134 MB).
+
+``value`` is the stage-1 useful TFLOP/s (QK^T over the visible keys, counted
+once); the max-pool and block-table bandwidths are in ``components``.  Each
+kernel's average duration comes from HIP events recorded on torch's current
+stream, the stream the kernels are launched on.  ``cpu_baseline`` times the CPU
+oracle (the reference algorithm restated in torch/numpy) on a bounded sample on
+this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+METRIC = ("stage1 TFLOP/s (% bf16 MFMA peak); maxpool+block-table GB/s (% HBM) @32K")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU oracle timing (e.g. under a profiler)")
+    ap.add_argument("--only", choices=["stage1", "maxpool", "block_table"], default=None,
+                    help="run a single kernel (profiling)")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_inputs(dev):
+    import torch
+
+    from unum_ops_amd import workloads
+    from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
+
+    t0 = time.time()
+    s1 = workloads.cfg3_stage1()
+    s1g = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in s1.items()}
+    mp = workloads.cfg2_maxpool()
+    mpg = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in mp.items()}
+    log(f"cfg3/cfg2 inputs ready ({time.time() - t0:.1f}s)")
+    # block-table inputs: run the cfg5 pipeline up to top-k once (untimed)
+    p5 = workloads.cfg5_pipeline()
+    q5, k5 = p5["q"].to(dev), p5["k"].to(dev)
+    cu_q5, cu_k5 = p5["cu_seqlens_q"].to(dev), p5["cu_seqlens_k"].to(dev)
+    sc = infllmv2_attn_stage1(q5, k5, None, cu_q5, cu_k5, max_seqlen_k=p5["max_seqlen_k"],
+                              causal=True)
+    kp = sc.shape[-1]
+    pooled = max_pooling_1d_varlen(sc, cu_q5, cu_k5, torch.zeros(1, dtype=torch.int32, device=dev),
+                                   max_seqlen_q=16 * kp, max_context_len=p5["max_context_len"],
+                                   local_blocks=1, init_blocks=1)
+    topk = torch.topk(pooled, 64, dim=-1).indices.sort(-1).values.to(torch.int32)
+    bt = dict(topk_idx=topk, block_table=p5["block_table"].to(dev),
+              token_to_bs=p5["token_to_bs"].to(dev), token_pos_in_bs=p5["token_pos_in_bs"].to(dev),
+              seqlen_q=p5["seqlen_q"].to(dev))
+    del sc, pooled, q5, k5
+    torch.cuda.synchronize()
+    log(f"cfg5 block-table inputs ready ({time.time() - t0:.1f}s)")
+    return s1, s1g, mp, mpg, bt
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the selection path shards by kv head or by sequence with no exchange, "
+              "so multi-GPU throughput is not measured here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from unum_ops_amd import workloads
+    from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
+    from unum_ops_amd.sparse_kernel_extension import get_block_table
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    s1, s1g, mp, mpg, bt = build_inputs(dev)
+    mp_kw = {k: mp[k] for k in ("max_seqlen_q", "max_context_len", "local_blocks",
+                                "init_blocks", "block_size", "stride")}
+
+    def op_stage1():
+        return infllmv2_attn_stage1(s1g["q"], s1g["k"], None, s1g["cu_seqlens_q"],
+                                    s1g["cu_seqlens_k"], max_seqlen_k=s1g["max_seqlen_k"],
+                                    causal=True)
+
+    def op_maxpool():
+        return max_pooling_1d_varlen(mpg["input"], mpg["cu_seqlens_q"], mpg["cu_seqlens_k"],
+                                     mpg["cache_lens"], **mp_kw)
+
+    def op_block_table():
+        return get_block_table(bt["topk_idx"], bt["block_table"], bt["token_to_bs"],
+                               bt["token_pos_in_bs"], bt["seqlen_q"])
+
+    ops = [("stage1", op_stage1), ("maxpool", op_maxpool), ("block_table", op_block_table)]
+    if args.only:
+        ops = [o for o in ops if o[0] == args.only]
+
+    for _ in range(args.warmup):
+        for _, fn in ops:
+            fn()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in ops] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for i, (_, fn) in enumerate(ops):
+            ev[s][i][0].record()
+            fn()
+            ev[s][i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_op = {name: sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps))
+              / args.steps for i, (name, _) in enumerate(ops)}          # ms
+    log("timed: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in per_op.items()))
+
+    comps = {}
+    if "stage1" in per_op:
+        flop, nbytes, _ = workloads.stage1_work(s1["cu_seqlens_q"], s1["cu_seqlens_k"], 32, 2,
+                                                128, 512)
+        t = per_op["stage1"] * 1e-3
+        comps["stage1"] = dict(us=per_op["stage1"] * 1e3, tflops=flop / t / 1e12,
+                               pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                               gbs=nbytes / t / 1e9, pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                               flop=flop, bytes=nbytes, bound="hbm",
+                               config="cfg3 4x8192 causal, Hq32/Hkv2/D128, fp32 out [2,32768,512]")
+    if "maxpool" in per_op:
+        nbytes = workloads.maxpool_bytes(mp["cu_seqlens_q"], mp["cu_seqlens_k"], mp["cache_lens"],
+                                         2, 256)
+        t = per_op["maxpool"] * 1e-3
+        comps["maxpool"] = dict(us=per_op["maxpool"] * 1e3, gbs=nbytes / t / 1e9,
+                                pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
+                                config="cfg2 q {4096,6144,8192,16384}, fp32 [2,34816,1024]->[2,34816,256]")
+    if "block_table" in per_op:
+        nbytes = workloads.block_table_bytes(bt["topk_idx"].cpu(), bt["token_to_bs"].cpu(), 2,
+                                             4096, 64, 1)
+        t = per_op["block_table"] * 1e-3
+        comps["block_table"] = dict(us=per_op["block_table"] * 1e3, gbs=nbytes / t / 1e9,
+                                    pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                    bytes=nbytes,
+                                    config="cfg5 block-table stage: T=4096 H=2 K=64 -> int32 [4096,2,4096]")
+
+    cpu = None
+    if not args.no_cpu_baseline and "stage1" in comps:
+        cpu = cpu_baseline(s1)
+
+    s1c = comps.get("stage1")
+    line = {
+        "metric": METRIC,
+        "value": round(s1c["tflops"], 3) if s1c else None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.Generator('cpu'), BASELINE.json configs)",
+        "config": {"workload": "selection path @32K: stage1 cfg3 + maxpool cfg2 + "
+                               "block table cfg5 (headline value: stage1 cfg3)",
+                   "stage1": "cfg3", "maxpool": "cfg2", "block_table": "cfg5 stage",
+                   "parallelism": "single GPU"},
+        "components": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                           for kk, vv in v.items()} for k, v in comps.items()},
+    }
+    if s1c:
+        line["roofline"] = {"bound": "hbm", "achieved": round(s1c["gbs"], 1),
+                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(s1c["gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                            "kernel": "stage1 (cfg3)",
+                            "mfma_frac": round(s1c["tflops"] / PEAK_BF16_TFLOPS, 4)}
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(s1):
+    """The CPU oracle (torch fp32, reference algorithm) on one 8192-token sequence of cfg3."""
+    import torch
+
+    from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
+    from unum_ops_amd import workloads
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    q = s1["q"][:8192]
+    k = s1["k"][:511]
+    cu_q = torch.tensor([0, 8192], dtype=torch.int32)
+    cu_k = torch.tensor([0, 511], dtype=torch.int32)
+    flop, _, _ = workloads.stage1_work(cu_q, cu_k, 32, 2, 128, 512)
+    oracle_stage1(q[:512], k, None, torch.tensor([0, 512], dtype=torch.int32), cu_k,
+                  max_seqlen_k=511, causal=True)                      # warm-up
+    times = []
+    t_end = time.time() + 25
+    while len(times) < 3 or (len(times) < 5 and time.time() < t_end):
+        t0 = time.perf_counter()
+        oracle_stage1(q, k, None, cu_q, cu_k, max_seqlen_k=511, causal=True)
+        times.append(time.perf_counter() - t0)
+        if time.time() > t_end:
+            break
+    med = sorted(times)[len(times) // 2]
+    log(f"cpu baseline: {med:.2f} s per 8192-token sequence ({len(times)} runs)")
+    return {"value": round(flop / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": "oracle stage 1 (torch fp32 CPU) on one 8192-token sequence of cfg3 "
+                      f"(1/4 of the workload), median of {len(times)} runs"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,146 @@
+/*
+ * unum_ops_amd -- C ABI of the MI355X (gfx950) InfLLM-v2 selection path.
+ *
+ * Plain C: raw device pointers, element strides and sizes, a HIP stream passed
+ * as `void*` (a `hipStream_t`), and an int status.  No torch types cross this
+ * boundary.  The library never allocates, frees or synchronises: every
+ * launch is asynchronous on `stream`; outputs and workspaces are owned by the
+ * caller.  Kernels are compiled for gfx950 only.
+ *
+ * Status: UNUM_OK (0) on success, a negative UNUM_ERR_* code otherwise; the
+ * thread-local message of the last failure is returned by unum_last_error().
+ *
+ * Reference interfaces replaced (paths relative to Yanguan619/unum_ops):
+ *   unum_infllmv2_attn_stage1  <- infllmv2_attn_stage1 =
+ *       src/unum_ops/infllm_v2/infllmv2_attn_stage1_triton_v2.py:153-228
+ *       (exported at src/unum_ops/infllm_v2/__init__.py:3-5)
+ *   unum_max_pooling_1d_varlen <- max_pooling_1d_varlen =
+ *       src/unum_ops/infllm_v2/max_pooling_1d_varlen.py:127-183
+ *       (exported at src/unum_ops/infllm_v2/__init__.py:7-9)
+ *   unum_get_block_table       <- get_block_table_ref_torch
+ *       src/unum_ops/sparse_kernel_extension/get_table_torch.py:4-44 and the
+ *       exported get_block_table_v2/_v3 (sparse_kernel_extension/__init__.py:7-12
+ *       -> get_table_triton.py:218-264)
+ */
+#ifndef UNUM_OPS_AMD_H_
+#define UNUM_OPS_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UNUM_ABI_VERSION 1
+
+enum unum_status {
+  UNUM_OK = 0,
+  UNUM_ERR_INVALID_ARGUMENT = -1, /* shape / stride / value outside the contract */
+  UNUM_ERR_UNSUPPORTED = -2,      /* a combination no kernel implements         */
+  UNUM_ERR_WORKSPACE = -3,        /* workspace missing or too small             */
+  UNUM_ERR_LAUNCH = -4,           /* the HIP runtime rejected a launch          */
+};
+
+enum unum_dtype {
+  UNUM_DTYPE_F32 = 0,
+  UNUM_DTYPE_BF16 = 1,
+  UNUM_DTYPE_F16 = 2,
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* unum_last_error(void);
+
+/* UNUM_ABI_VERSION of the built library. */
+int unum_abi_version(void);
+
+/*
+ * Stage-1 block scores (InfLLM-v2), replacing infllmv2_attn_stage1
+ * (infllmv2_attn_stage1_triton_v2.py:153-228, kernel :20-150).
+ *
+ *   q   bf16 [Tq, Hq, D]   element strides (q_stride_t, q_stride_h, 1)
+ *   k   bf16 [Tk, Hkv, D]  element strides (k_stride_t, k_stride_h, 1)
+ *   cu_seqlens_q / cu_seqlens_k  int32 [B+1] prefix sums
+ *   out [Hkv, Tq, out_cols] contiguous, dtype out_dtype (F32 or BF16);
+ *       out_cols = round_up(max_seqlen_k, 128) in the reference.
+ *
+ * For token t of sequence b and kv group g (G = Hq / Hkv heads):
+ *   out[g, t, j] = sum_{i<G} softmax_j(scale * q[t, gG+i] . k[cu_k[b]+j, g])
+ * over the visible keys j < vis(t) (causal rule of the reference, truncating
+ * division), 0 for vis <= j < out_cols, and 0 for the whole row when
+ * vis == 0 or the sequence has no keys.  Every element of `out` is written.
+ *
+ * `workspace` must hold unum_infllmv2_attn_stage1_workspace_size(...) bytes
+ * (it may be NULL when that size is 0).
+ */
+int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                              const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              void* out, int32_t out_dtype, int64_t B, int64_t Tq,
+                              int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
+                              int64_t max_seqlen_k, int64_t out_cols, float scale,
+                              int32_t causal, void* workspace, int64_t workspace_bytes,
+                              void* stream);
+
+/* Workspace bytes unum_infllmv2_attn_stage1 needs for this problem (>= 0). */
+int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t Hq,
+                                                 int64_t Hkv, int64_t D,
+                                                 int64_t max_seqlen_k);
+
+/*
+ * Varlen 1-D max-pool of compressed-block scores, replacing
+ * max_pooling_1d_varlen (max_pooling_1d_varlen.py:127-183, kernel :33-124).
+ *
+ *   input  [H, Tq, *] of dtype `dtype` (F32, BF16 or F16), read FLAT:
+ *          tap p of row (h, t) is input_flat[(h*Tq + t) * flat_stride + p]
+ *          with flat_stride = max_seqlen_q / stride (the reference's
+ *          convention); input_numel bounds every read.
+ *   cu_seqlens_q / cu_seqlens_k int32 [B+1], cache_lens int32 [B]
+ *   out    [H, Tq, num_blocks] contiguous, same dtype as input.
+ *
+ * Window n covers taps n*P-1 .. n*P+P-1 (P = block_size / stride, padding 1)
+ * that fall in [0, Lk), Lk = cu_k[b+1]-cu_k[b]+cache_lens[b]; +inf for
+ * n < init_blocks or n <= (t-cu_q[b])/block_size <= n+local_blocks; -inf for an
+ * empty window.  A tap whose flat address is >= input_numel is treated as
+ * absent (the reference reads out of bounds there).
+ */
+int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel, int32_t dtype,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                               const int32_t* cache_lens, void* out, int64_t H,
+                               int64_t Tq, int64_t B, int64_t flat_stride,
+                               int64_t num_blocks, int32_t block_size, int32_t stride,
+                               int32_t local_blocks, int32_t init_blocks, void* stream);
+
+/*
+ * Top-k block ids -> per-token paged KV slots, replacing
+ * get_block_table_ref_torch (get_table_torch.py:4-44) and the exported
+ * get_block_table_v2/_v3 (get_table_triton.py:218-264, kernel :6-67).
+ *
+ *   topk_idx    int32 [H, T, K], element strides (s_h, s_t, s_k)
+ *   block_table int32 [B, L], row stride bt_stride_b, unit column stride
+ *   token_to_bs int32 [T]
+ *   token_pos_in_bs int32 [T] or one element (pos_numel == 1 broadcasts)
+ *   seqlen_q    int32 [>= B] indexed by b, or one element (seqlen_numel == 1
+ *               broadcasts)
+ *   out         int32 [T, H, K*64] contiguous
+ *
+ *   p = topk_idx[h,t,k]*64 + o (int32, wrapping), b = token_to_bs[t]
+ *   out[t,h,64k+o] = (p >= 0 && p < seqlen[b] && p < pos[t])
+ *                    ? head_group * block_table[b, min(p, L-1)] + h : 0
+ * head_group is 2 in the torch reference (kHeadGroup) and H in the Triton
+ * kernels; they agree for H == 2.  A token whose token_to_bs is outside
+ * [0, B) gets an all-zero row (the reference raises or reads out of bounds).
+ * Every element of `out` is written.
+ */
+int unum_get_block_table(const int32_t* topk_idx, int64_t topk_stride_h,
+                         int64_t topk_stride_t, int64_t topk_stride_k,
+                         const int32_t* block_table, int64_t bt_stride_b,
+                         const int32_t* token_to_bs, const int32_t* token_pos_in_bs,
+                         int64_t pos_numel, const int32_t* seqlen_q, int64_t seqlen_numel,
+                         int32_t* out, int64_t H, int64_t T, int64_t K, int64_t B,
+                         int64_t L, int32_t head_group, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNUM_OPS_AMD_H_ */

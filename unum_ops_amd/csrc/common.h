@@ -1,0 +1,72 @@
+// Shared helpers for the gfx950 kernels and their C-ABI launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/unum_ops_amd.h"
+
+namespace unum {
+
+// Thread-local message of the last failing C-ABI call (capi.hip owns it).
+void set_error(const char* fmt, ...);
+void clear_error();
+
+// Validation helper: record the message and return `code`.
+#define UNUM_FAIL(code, ...)          \
+  do {                                \
+    ::unum::set_error(__VA_ARGS__);   \
+    return (code);                    \
+  } while (0)
+
+#define UNUM_REQUIRE(cond, ...)                                        \
+  do {                                                                 \
+    if (!(cond)) UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, __VA_ARGS__);    \
+  } while (0)
+
+// Check the launch that was just enqueued.
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return UNUM_ERR_LAUNCH;
+  }
+  return UNUM_OK;
+}
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+}  // namespace unum
