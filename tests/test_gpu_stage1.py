@@ -118,7 +118,10 @@ def test_cfg3_full_size_properties(dev):
     sums = out.sum(-1).cpu()
     vis = np.concatenate([visible_counts(np.arange(8192), 8192, 511)] * 4)
     exp = torch.where(torch.from_numpy(vis) > 0, 16.0, 0.0).float()
-    torch.testing.assert_close(sums, exp.expand(2, -1), atol=2e-3, rtol=0)
+    # The head sum runs on the matrix core with the exponentials and 1/l in
+    # f16 (relative rounding 2^-11 each), so a row sum of 16 carries up to
+    # ~16 * 5e-4 of rounding; 1e-2 bounds it with margin.
+    torch.testing.assert_close(sums, exp.expand(2, -1), atol=1e-2, rtol=0)
     cols = torch.arange(512, device=dev)
     mask = cols[None, :] >= torch.from_numpy(vis).to(dev)[:, None]
     assert torch.all(out[:, mask] == 0)

@@ -4,13 +4,14 @@
 // (src/unum_ops/sparse_kernel_extension/get_table_torch.py:4-44); the exported
 // Triton kernel (get_table_triton.py:6-67) computes the same gather.
 //
-// Work decomposition: the output [T, H, K*64] int32 is a flat array of
-// "items" (t, h, k), each a 64-entry run.  One thread owns four consecutive
-// entries of one item, so a 64-lane wave writes four whole items (1 KiB) with
-// one dwordx4 store per lane; the block-table gather for those entries is one
-// dwordx4 load when the four positions are valid, in range and 16-byte
-// aligned.  The kernel is bound by the output write (see the roofline note in
-// the launcher).
+// Work decomposition: one wave owns one (token, head) row of the output --
+// K runs of 64 entries.  The per-token scalars (sequence, position limit,
+// sequence length) are read once per wave; the row's ids are read 64 at a
+// time, one per lane, and broadcast with a lane shuffle; each store step
+// writes four whole runs (1 KiB, one dwordx4 per lane).  The block-table
+// gather for those entries is one dwordx4 load when the four positions are
+// valid, in range and 16-byte aligned.  The kernel is bound by the output
+// write.
 #include "common.h"
 
 namespace unum {
@@ -30,7 +31,6 @@ struct BlockTableArgs {
   int32_t H, T, K, B, L;
   int32_t pos_scalar, seqlen_scalar;
   int32_t head_group;
-  int64_t n_quads;  // T*H*K*16
 };
 
 __device__ __forceinline__ int32_t wrap_add_i32(int32_t a, int32_t b) {
@@ -40,51 +40,87 @@ __device__ __forceinline__ int32_t wrap_mul_i32(int32_t a, int32_t b) {
   return static_cast<int32_t>(static_cast<uint32_t>(a) * static_cast<uint32_t>(b));
 }
 
-template <bool kVecTable>
-__global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a) {
-  const int64_t quad = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (quad >= a.n_quads) return;
-  const int32_t item = static_cast<int32_t>(quad >> 4);  // (t*H + h)*K + k
-  const int32_t o0 = static_cast<int32_t>(quad & 15) * 4;
-  const int32_t k = item % a.K;
-  const int32_t th = item / a.K;
-  const int32_t h = th % a.H;
-  const int32_t t = th / a.H;
-
-  i32x4 res = {0, 0, 0, 0};
-  const int32_t b = a.token_to_bs[t];
-  if (b >= 0 && b < a.B) {
-    const int32_t idx = a.topk[h * a.s_h + t * a.s_t + k * a.s_k];
-    const int32_t limit_pos = a.pos[a.pos_scalar ? 0 : t];
-    const int32_t limit_len = a.seqlen[a.seqlen_scalar ? 0 : b];
-    const int32_t p0 = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
-    const int32_t* row = a.bt + static_cast<int64_t>(b) * a.bt_stride;
-    int32_t p[4];
-    bool valid[4];
-    bool all_fast = true;
+// Finish four entries of a run from the dwordx4 `raw` loaded at the clamped
+// address `safe`: entries whose position the vector covered take it, the
+// others (positions outside [0, L-4], the clamp to L-1) read the table one by
+// one.  Invalid entries are 0.
+__device__ __forceinline__ i32x4 finish4(const BlockTableArgs& a, const int32_t* row, i32x4 raw,
+                                         bool raw_ok, int32_t p0, int32_t limit_len,
+                                         int32_t limit_pos, int32_t h) {
+  int32_t p[4];
+  bool valid[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    p[e] = wrap_add_i32(p0, e);
+    valid[e] = p[e] >= 0 && p[e] < limit_len && p[e] < limit_pos;
+  }
+  int32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
+  if (!raw_ok) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      p[e] = wrap_add_i32(p0, e);
-      valid[e] = p[e] >= 0 && p[e] < limit_len && p[e] < limit_pos;
-      all_fast = all_fast && valid[e] && p[e] < a.L;
+      const int32_t c = p[e] < 0 ? 0 : (p[e] > a.L - 1 ? a.L - 1 : p[e]);
+      v[e] = valid[e] ? row[c] : 0;
     }
-    int32_t v[4];
-    if (kVecTable && all_fast) {  // all four valid and < L: p0..p0+3 consecutive
-      const i32x4 w = *reinterpret_cast<const i32x4*>(row + p0);
-      v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
-    } else {
+  }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int32_t c = p[e] < 0 ? 0 : (p[e] > a.L - 1 ? a.L - 1 : p[e]);
-        v[e] = valid[e] ? row[c] : 0;
+  for (int e = 0; e < 4; ++e)
+    v[e] = valid[e] ? wrap_add_i32(wrap_mul_i32(a.head_group, v[e]), h) : 0;
+  return i32x4{v[0], v[1], v[2], v[3]};
+}
+
+template <bool kVecTable>
+__global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a) {
+  const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // t*H + h
+  if (th >= static_cast<int64_t>(a.T) * a.H) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t t = static_cast<int32_t>(th / a.H);
+  const int32_t h = static_cast<int32_t>(th - static_cast<int64_t>(t) * a.H);
+  i32x4* out = reinterpret_cast<i32x4*>(a.out + th * a.K * kSparseBlock);
+  const int32_t sub = lane >> 4;            // run within a store step
+  const int32_t o0 = (lane & 15) * 4;       // first entry of the lane in its run
+  const int32_t b = a.token_to_bs[t];
+  if (b < 0 || b >= a.B) {
+    for (int32_t q = lane; q < a.K * 16; q += kWave) out[q] = i32x4{0, 0, 0, 0};
+    return;
+  }
+  const int32_t limit_pos = a.pos[a.pos_scalar ? 0 : t];
+  const int32_t limit_len = a.seqlen[a.seqlen_scalar ? 0 : b];
+  const int32_t* row = a.bt + static_cast<int64_t>(b) * a.bt_stride;
+  const int32_t* ids = a.topk + static_cast<int64_t>(h) * a.s_h + static_cast<int64_t>(t) * a.s_t;
+  const int32_t vec_hi = a.L - 4;  // a dwordx4 at p0 (a multiple of 4) covers p0..p0+3 <= L-1
+  for (int32_t kb = 0; kb < a.K; kb += kWave) {
+    const int32_t my = (kb + lane < a.K) ? ids[static_cast<int64_t>(kb + lane) * a.s_k] : -1;
+    if (kVecTable && a.K - kb >= kWave) {
+      // Sixteen store steps of four runs each; all table loads go out first.
+      int32_t p0[16];
+      i32x4 raw[16];
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const int32_t idx = __shfl(my, 4 * st + sub);
+        p0[st] = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
+        const int32_t safe = (p0[st] >= 0 && p0[st] <= vec_hi) ? p0[st] : 0;
+        raw[st] = *reinterpret_cast<const i32x4*>(row + safe);
+      }
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const bool raw_ok = p0[st] >= 0 && p0[st] <= vec_hi;
+        out[static_cast<int64_t>(kb + 4 * st + sub) * 16 + (lane & 15)] =
+            finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h);
+      }
+    } else {
+      const int32_t steps = (a.K - kb) < kWave ? (a.K - kb + 3) / 4 : kWave / 4;
+      for (int32_t st = 0; st < steps; ++st) {
+        const int32_t k = kb + 4 * st + sub;
+        const int32_t idx = __shfl(my, 4 * st + sub);
+        const int32_t q0 = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
+        const bool raw_ok = kVecTable && q0 >= 0 && q0 <= vec_hi;
+        const i32x4 raw = raw_ok ? *reinterpret_cast<const i32x4*>(row + q0) : i32x4{0, 0, 0, 0};
+        if (k < a.K)
+          out[static_cast<int64_t>(k) * 16 + (lane & 15)] =
+              finish4(a, row, raw, raw_ok, q0, limit_len, limit_pos, h);
       }
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v[e] = valid[e] ? wrap_add_i32(wrap_mul_i32(a.head_group, v[e]), h) : 0;
-    res = i32x4{v[0], v[1], v[2], v[3]};
   }
-  *reinterpret_cast<i32x4*>(a.out + static_cast<int64_t>(item) * kSparseBlock + o0) = res;
 }
 
 }  // namespace
@@ -140,13 +176,14 @@ extern "C" int unum_get_block_table(const int32_t* topk_idx, int64_t topk_stride
   a.pos_scalar = pos_numel == 1;
   a.seqlen_scalar = seqlen_numel == 1;
   a.head_group = head_group;
-  a.n_quads = n_items * 16;
 
   UNUM_REQUIRE((reinterpret_cast<uintptr_t>(out) & 15) == 0,
                "get_block_table: output must be 16-byte aligned");
-  const bool vec = (reinterpret_cast<uintptr_t>(block_table) & 15) == 0 && (bt_stride_b % 4) == 0;
-  const int threads = 256;
-  const int64_t blocks = (a.n_quads + threads - 1) / threads;
+  const bool vec = (reinterpret_cast<uintptr_t>(block_table) & 15) == 0 && (bt_stride_b % 4) == 0 &&
+                   L >= 4;
+  const int threads = 256;  // four (token, head) rows per block
+  const int64_t blocks = (T * H + 3) / 4;
+  UNUM_REQUIRE(blocks <= INT32_MAX, "get_block_table: T*H=%lld too large", (long long)(T * H));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (vec)
     hipLaunchKernelGGL(block_table_kernel<true>, dim3((unsigned)blocks), dim3(threads), 0, s, a);

@@ -3,16 +3,15 @@
 // Reference semantics: the Triton kernel _max_pooling_1d_varlen_kernel and its
 // wrapper (src/unum_ops/infllm_v2/max_pooling_1d_varlen.py:33-183).
 //
-// Work decomposition: one wave owns a 256-output chunk of one row (h, t);
-// lane i owns outputs n0..n0+3 with n0 = 256*chunk + 4i.  With the reference's
-// block_size 64 / stride 16 (P = 4 taps per step, 5-tap windows, padding 1)
-// those four windows cover taps 4*n0-1 .. 4*n0+15: sixteen consecutive input
-// elements that the lane reads as 16-byte vectors, plus the one tap before
-// them.  A wave therefore streams one contiguous 1024-element stretch of the
-// row in and one 256-element stretch of the output out, with every input
-// element read from HBM once -- the kernel is bound by HBM bandwidth.  The
-// row -> sequence lookup is one 64-lane vector load of cu_seqlens_q and a
-// ballot, done once per wave.
+// Work decomposition: one wave owns a 256-output chunk of one row (h, t) and
+// walks it in four steps of 64 outputs, one output n per lane.  With the
+// reference's block_size 64 / stride 16 (P = 4 taps per step, 5-tap windows,
+// padding 1) window n covers taps 4n-1 .. 4n+3: the lane reads taps 4n..4n+3
+// as one vector -- a wave's load is one contiguous 1 KiB (fp32) -- and takes
+// tap 4n-1 from the lane below (lane 0 from the previous step).  Every input
+// element is read from HBM once and every output written once, so the kernel
+// is bound by HBM bandwidth.  The row -> sequence lookup is one 64-lane
+// vector load of cu_seqlens_q and a ballot, done once per wave.
 #include "common.h"
 
 namespace unum {
@@ -28,7 +27,7 @@ struct PoolArgs {
   int64_t H, Tq, B, F, NB;
   int32_t block_size, P, local_blocks, init_blocks;
   int64_t n_chunks;  // chunks of 256 outputs per row
-  int64_t n_waves;   // H * Tq * n_chunks
+  int64_t n_units;   // (row, chunk) units: H * Tq * n_chunks
 };
 
 template <typename T>
@@ -77,107 +76,111 @@ __device__ __forceinline__ int find_sequence(const int32_t* cu_q, int64_t B, int
   return (t < cu_q[b + 1]) ? b : -1;
 }
 
-// Fast path: P == 4 (block_size / stride), vector loads and stores allowed.
+template <typename T>
+struct Vec4;
+template <>
+struct Vec4<float> {
+  static __device__ __forceinline__ f32x4 load(const void* p, int64_t i) {
+    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  }
+};
+template <>
+struct Vec4<__bf16> {
+  static __device__ __forceinline__ f32x4 load(const void* p, int64_t i) {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                 __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+  }
+};
+template <>
+struct Vec4<_Float16> {
+  static __device__ __forceinline__ f32x4 load(const void* p, int64_t i) {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    return f32x4{f16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu)),
+                 f16_bits_to_f32(static_cast<uint16_t>(w.x >> 16)),
+                 f16_bits_to_f32(static_cast<uint16_t>(w.y & 0xffffu)),
+                 f16_bits_to_f32(static_cast<uint16_t>(w.y >> 16))};
+  }
+};
+
+// Fast path: P == 4 (block_size / stride == 4).  A wave processes kUnits
+// consecutive (row, 256-output chunk) units; every input load of all units is
+// issued before the first one is used, so a wave keeps 16 KiB of reads in
+// flight.
+constexpr int kUnits = 4;
+
 template <typename T, bool kVec>
 __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (wave >= a.n_waves) return;  // wave-uniform
+  const int64_t u0 = wave * kUnits;
+  if (u0 >= a.n_units) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = wave / a.n_chunks;  // h*Tq + t
-  const int64_t chunk = wave - row * a.n_chunks;
-  const int64_t t = row % a.Tq;
 
-  const int b = find_sequence(a.cu_q, a.B, t);
-  int64_t lk = 0, ob = 0;
-  if (b >= 0) {
-    lk = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
-    ob = (t - a.cu_q[b]) / a.block_size;
-  }
-  const int64_t base = row * a.F;
-  // Taps beyond either the key length or the end of the input are absent.
-  const int64_t lim = lk < (a.numel - base) ? lk : (a.numel - base);
-
-  const int64_t n0 = chunk * 256 + 4 * lane;
-  if (n0 >= a.NB) return;
-  const int64_t p0 = 4 * n0;  // first of the 16 taps owned by this lane
-
-  float v[17];  // v[0] = tap p0-1, v[1+j] = tap p0+j
-  if (kVec && p0 + 15 < lim) {
-    const T* src = static_cast<const T*>(a.in) + base + p0;
-    if constexpr (sizeof(T) == 4) {
+  f32x4 v[kUnits][4];
+  float carry[kUnits];
+  int64_t lk[kUnits], ob[kUnits], out_base[kUnits], nfirst[kUnits];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 w = reinterpret_cast<const f32x4*>(src)[q];
-        v[1 + 4 * q] = w.x; v[2 + 4 * q] = w.y; v[3 + 4 * q] = w.z; v[4 + 4 * q] = w.w;
-      }
+  for (int i = 0; i < kUnits; ++i) {
+    const int64_t u = u0 + i < a.n_units ? u0 + i : a.n_units - 1;  // tail: redo the last unit
+    const int64_t row = u / a.n_chunks;  // h*Tq + t
+    const int64_t chunk = u - row * a.n_chunks;
+    const int64_t t = row % a.Tq;
+    const int b = find_sequence(a.cu_q, a.B, t);
+    lk[i] = 0;
+    ob[i] = 0;
+    if (b >= 0) {
+      lk[i] = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
+      ob[i] = (t - a.cu_q[b]) / a.block_size;
+    }
+    const int64_t base = row * a.F;
+    // Taps are present below the key length, inside the input, and below the
+    // last tap any output window uses (4*NB - 1).
+    int64_t lim = lk[i] < (a.numel - base) ? lk[i] : (a.numel - base);
+    lim = lim < 4 * a.NB ? lim : 4 * a.NB;
+    nfirst[i] = chunk * 256;
+    out_base[i] = row * a.NB;
+    const int64_t p_first = 4 * nfirst[i];
+    {
+      const int64_t p = p_first - 1;
+      carry[i] = (p >= 0 && p < lim) ? Elem<T>::load(a.in, base + p) : -INFINITY;
+    }
+    if (kVec && p_first + 1023 < lim) {  // the whole chunk is present: plain vector loads
+#pragma unroll
+      for (int st = 0; st < 4; ++st) v[i][st] = Vec4<T>::load(a.in, base + p_first + 256 * st + 4 * lane);
     } else {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const i32x4 w = reinterpret_cast<const i32x4*>(src)[q];
-        const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint16_t lo = static_cast<uint16_t>(u[e] & 0xffffu);
-          const uint16_t hi = static_cast<uint16_t>(u[e] >> 16);
-          if constexpr (sizeof(T) == 2 && __is_same(T, __bf16)) {
-            v[1 + 8 * q + 2 * e] = bf16_bits_to_f32(lo);
-            v[2 + 8 * q + 2 * e] = bf16_bits_to_f32(hi);
-          } else {
-            v[1 + 8 * q + 2 * e] = f16_bits_to_f32(lo);
-            v[2 + 8 * q + 2 * e] = f16_bits_to_f32(hi);
-          }
+      for (int st = 0; st < 4; ++st) {
+        const int64_t p0 = p_first + 256 * st + 4 * lane;
+        if (kVec && p0 + 3 < lim) {
+          v[i][st] = Vec4<T>::load(a.in, base + p0);
+        } else {
+          v[i][st].x = (p0 + 0 < lim) ? Elem<T>::load(a.in, base + p0 + 0) : -INFINITY;
+          v[i][st].y = (p0 + 1 < lim) ? Elem<T>::load(a.in, base + p0 + 1) : -INFINITY;
+          v[i][st].z = (p0 + 2 < lim) ? Elem<T>::load(a.in, base + p0 + 2) : -INFINITY;
+          v[i][st].w = (p0 + 3 < lim) ? Elem<T>::load(a.in, base + p0 + 3) : -INFINITY;
         }
       }
     }
-  } else {
+  }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int64_t p = p0 + j;
-      v[1 + j] = (p < lim) ? Elem<T>::load(a.in, base + p) : -INFINITY;
+  for (int i = 0; i < kUnits; ++i) {
+    if (u0 + i >= a.n_units) break;
+    float cy = carry[i];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const f32x4 w = v[i][st];
+      float prev = __shfl_up(w.w, 1);
+      prev = lane == 0 ? cy : prev;
+      cy = __shfl(w.w, kWave - 1);
+      const float m = fmaxf(fmaxf(fmaxf(prev, w.x), fmaxf(w.y, w.z)), w.w);
+      const int64_t n = nfirst[i] + 64 * st + lane;
+      const int64_t ws = 4 * n - 1;
+      const int64_t w_lo = ws < 0 ? 0 : ws;
+      const int64_t w_hi = (ws + 5) < lk[i] ? (ws + 5) : lk[i];
+      const bool force = n < a.init_blocks || (ob[i] >= n && ob[i] <= n + a.local_blocks);
+      const float r = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
+      if (n < a.NB) Elem<T>::store(a.out, out_base[i] + n, r);
     }
-  }
-  {
-    const int64_t p = p0 - 1;
-    v[0] = (p >= 0 && p < lim) ? Elem<T>::load(a.in, base + p) : -INFINITY;
-  }
-
-  float r[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t n = n0 + e;
-    float m = v[4 * e];
-#pragma unroll
-    for (int j = 1; j < 5; ++j) m = fmaxf(m, v[4 * e + j]);
-    const int64_t ws = 4 * n - 1;
-    const int64_t w_lo = ws < 0 ? 0 : ws;
-    const int64_t w_hi = (ws + 5) < lk ? (ws + 5) : lk;
-    const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
-    r[e] = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
-  }
-
-  const int64_t o = row * a.NB + n0;
-  if (kVec && n0 + 3 < a.NB) {
-    if constexpr (sizeof(T) == 4) {
-      *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + o) = f32x4{r[0], r[1], r[2], r[3]};
-    } else {
-      uint16_t h[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float tmp = r[e];
-        uint16_t bits;
-        if constexpr (__is_same(T, __bf16)) bits = f32_to_bf16_bits(tmp);
-        else bits = f32_to_f16_bits(tmp);
-        h[e] = bits;
-      }
-      uint2 pk;
-      pk.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-      pk.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + o) = pk;
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (n0 + e < a.NB) Elem<T>::store(a.out, o + e, r[e]);
   }
 }
 
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
 template <typename T>
 __global__ __launch_bounds__(256) void maxpool_generic_kernel(PoolArgs a) {
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (wave >= a.n_waves) return;
+  if (wave >= a.n_units) return;
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = wave / a.n_chunks;
   const int64_t chunk = wave - row * a.n_chunks;
@@ -218,16 +221,16 @@ __global__ __launch_bounds__(256) void maxpool_generic_kernel(PoolArgs a) {
 template <typename T>
 int launch_pool(const PoolArgs& a, hipStream_t s) {
   const int threads = 256;
-  const int64_t blocks = (a.n_waves * kWave + threads - 1) / threads;
+  const int64_t blocks = (a.n_units * kWave + threads - 1) / threads;  // generic: one wave per unit
   if (blocks > INT32_MAX) UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen: too many rows");
   if (a.P == 4) {
-    const bool vec = (reinterpret_cast<uintptr_t>(a.in) & 15) == 0 &&
-                     (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
-                     ((a.F * (int64_t)sizeof(T)) % 16) == 0 && (a.NB % 4) == 0;
+    const int64_t waves = (a.n_units + kUnits - 1) / kUnits;
+    const int64_t blocks4 = (waves * kWave + threads - 1) / threads;
+    const bool vec = (reinterpret_cast<uintptr_t>(a.in) & 15) == 0 && (a.F % 4) == 0;
     if (vec)
-      hipLaunchKernelGGL((maxpool_p4_kernel<T, true>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((maxpool_p4_kernel<T, true>), dim3((unsigned)blocks4), dim3(threads), 0, s, a);
     else
-      hipLaunchKernelGGL((maxpool_p4_kernel<T, false>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((maxpool_p4_kernel<T, false>), dim3((unsigned)blocks4), dim3(threads), 0, s, a);
   } else {
     hipLaunchKernelGGL((maxpool_generic_kernel<T>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
   }
@@ -279,7 +282,7 @@ extern "C" int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel
   a.local_blocks = local_blocks;
   a.init_blocks = init_blocks;
   a.n_chunks = (num_blocks + 255) / 256;
-  a.n_waves = H * Tq * a.n_chunks;
+  a.n_units = H * Tq * a.n_chunks;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case UNUM_DTYPE_F32: return launch_pool<float>(a, s);

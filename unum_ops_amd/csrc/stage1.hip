@@ -384,12 +384,411 @@ __global__ __launch_bounds__(64) void stage1_generic_kernel(Stage1Args a) {
   zero_tail<OutT>(orow, wr, a.out_cols);
 }
 
+// ----------------------------------------------------- LDS-resident K path
+// For sequences with at most kLdsTiles*16 = 512 compressed keys (the "32K"
+// prefill shapes), one persistent workgroup per CU keeps the whole compressed
+// K of one (sequence, group) in LDS -- 128 KiB, stored in MFMA B-fragment
+// order so a wave reads one 16x32 fragment with a single contiguous
+// ds_read_b128 -- and its eight waves each own whole (token, group) rows: the
+// row's score tiles stay in registers, the exact max is taken, and every
+// score is exponentiated once.
+//
+// Work split: the (group, token) rows of the batch are ordered by sequence,
+// then group, then token in zig-zag order (0, L-1, 1, L-2, ...), and each
+// workgroup takes one contiguous range of that order.  A range therefore
+// touches one or two (sequence, group) K blocks -- loaded once -- and its
+// causal work (which grows linearly with the token position) is balanced,
+// since consecutive zig-zag rows pair a short prefix with a long one.  Inside
+// a workgroup, waves take rows from an LDS counter and prefetch the next
+// row's query fragment while computing the current one.
+constexpr int kLdsWaves = 8;
+constexpr int kLdsTiles = 32;                    // 512 keys
+constexpr int kLdsUnits = kLdsTiles * 4 * kWave; // bf16x8 units: 128 KiB
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Reductions over the 16 lanes of a lane group (one head's keys of a tile):
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+__device__ __forceinline__ float grp_max16(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+__device__ __forceinline__ float grp_sum16(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return v;
+}
+
+// Per-lane head partials of four tiles (pa..pd) -> lane group u holds the full
+// head sum of tile u for key l%16 (two exchange steps instead of four
+// all-reduces).
+__device__ __forceinline__ float head_sum_quad(float pa, float pb, float pc, float pd) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool hi32 = lane >= 32;
+  const float send0 = hi32 ? pa : pc, send1 = hi32 ? pb : pd;
+  const float keep0 = hi32 ? pc : pa, keep1 = hi32 ? pd : pb;
+  const float x = keep0 + __shfl_xor(send0, 32);
+  const float y = keep1 + __shfl_xor(send1, 32);
+  const bool odd = (lane & 16) != 0;
+  return (odd ? y : x) + __shfl_xor(odd ? x : y, 16);
+}
+
+enum SegKind { kSeq = 0, kOrphan = 1, kSkip = 2 };
+
+struct Segment {
+  int64_t end;   // first row after the segment
+  int64_t k0;    // zig-zag position of the first row (sequence segments)
+  int32_t kind;  // SegKind
+  int32_t b, g;
+  int32_t qs, lq_len, ks, lk;
+  int64_t rlo, t0, nt_orphan;  // orphan segments: first row, first token, token count
+};
+
+// Rows are r in [0, Hkv*Tq): sequence b owns [Hkv*cu_q[b], Hkv*cu_q[b+1]),
+// group-major inside; rows before Hkv*cu_q[0] / after Hkv*cu_q[B] belong to
+// tokens outside every sequence (all-zero rows).
+__device__ Segment find_segment(const Stage1Args& a, int64_t r, int64_t r_end) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int count = 0;
+  for (int64_t base = 0; base <= a.B; base += kWave) {
+    const int64_t i = base + lane;
+    const bool le = (i <= a.B) && (static_cast<int64_t>(a.cu_q[i]) * a.Hkv <= r);
+    count += __popcll(__ballot(le));
+  }
+  Segment s;
+  s.kind = kSkip;
+  s.b = -1;
+  s.g = 0;
+  s.k0 = 0;
+  s.qs = s.lq_len = s.ks = s.lk = 0;
+  s.rlo = s.t0 = 0;
+  s.nt_orphan = 1;
+  const int b = count - 1;
+  const int64_t first = static_cast<int64_t>(a.cu_q[0]) * a.Hkv;
+  const int64_t last = static_cast<int64_t>(a.cu_q[a.B]) * a.Hkv;
+  if (b < 0 || r >= last || first < 0) {
+    // Orphan rows: tokens [0, cu_q[0]) or [cu_q[B], Tq), group-major.
+    const bool pre = b < 0;
+    const int64_t tlo = pre ? 0 : a.cu_q[a.B];
+    const int64_t thi = pre ? a.cu_q[0] : a.Tq;
+    const int64_t rlo = pre ? 0 : last;
+    const int64_t n = thi - tlo;
+    s.kind = n > 0 ? kOrphan : kSkip;
+    s.rlo = rlo;
+    s.t0 = tlo;
+    s.nt_orphan = n > 0 ? n : 1;
+    const int64_t rhi = rlo + a.Hkv * s.nt_orphan;
+    s.end = rhi < r_end ? rhi : r_end;
+    if (s.end <= r) s.end = r + 1;
+    return s;
+  }
+  const int32_t qs = a.cu_q[b], qe = a.cu_q[b + 1];
+  const int32_t Lq = qe - qs;
+  const int64_t off = r - static_cast<int64_t>(qs) * a.Hkv;
+  if (Lq <= 0 || off < 0) {  // malformed cu_seqlens_q: skip one row, write nothing
+    s.end = r + 1;
+    return s;
+  }
+  s.kind = kSeq;
+  s.b = b;
+  s.g = static_cast<int32_t>(off / Lq);
+  s.k0 = off - static_cast<int64_t>(s.g) * Lq;
+  s.qs = qs;
+  s.lq_len = Lq;
+  s.ks = a.cu_k[b];
+  s.lk = a.cu_k[b + 1] - s.ks;
+  const int64_t seg_hi = static_cast<int64_t>(qs) * a.Hkv + static_cast<int64_t>(s.g + 1) * Lq;
+  s.end = seg_hi < r_end ? seg_hi : r_end;
+  if (s.end <= r) s.end = r + 1;
+  return s;
+}
+
+__device__ __forceinline__ int64_t zigzag(int64_t k, int64_t L) {
+  return (k & 1) ? (L - 1 - (k >> 1)) : (k >> 1);
+}
+
+// K block (keys [0, 16*ntl), zero beyond lk) -> LDS in fragment order:
+// unit ((jt*4 + c)*64 + l) = k[ks + 16*jt + l%16][g][32*c + 8*(l/16) .. +8].
+// Each thread issues its (up to) 16 loads before writing any of them.
+__device__ __forceinline__ void load_k_block(const Stage1Args& a, bf16x8* kt, const Segment& sg,
+                                             int ntl) {
+  constexpr int kThreads = kLdsWaves * kWave;
+  constexpr int kPer = kLdsUnits / kThreads;  // 16
+  // An opaque copy of the thread index keeps the per-unit addresses from
+  // being hoisted out of the segment loop (and spilled) by the compiler.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int units = ntl * 4 * kWave;
+  const __bf16* kb = a.k + static_cast<int64_t>(sg.ks) * a.k_st + static_cast<int64_t>(sg.g) * a.k_sh;
+  const int64_t keys_ok = sg.lk < a.Tk - sg.ks ? sg.lk : a.Tk - sg.ks;  // keys inside k
+  bf16x8 v[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int u = tid + i * kThreads;
+    const int jt = u >> 8, cc = (u >> 6) & 3, l = u & 63;
+    const int key = 16 * jt + (l & 15);
+    v[i] = bf16x8{};
+    if (u < units && key < keys_ok && sg.ks + key >= 0)
+      v[i] = *reinterpret_cast<const bf16x8*>(kb + key * a.k_st + 32 * cc + 8 * (l >> 4));
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int u = tid + i * kThreads;
+    if (u < units) kt[u] = v[i];
+  }
+}
+
+template <typename OutT>
+__device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t cols) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if constexpr (sizeof(OutT) == 4) {
+    if ((cols & 3) == 0 && (from & 3) == 0) {
+      for (int64_t j = from + 4 * lane; j < cols; j += 4 * kWave)
+        *reinterpret_cast<f32x4*>(orow + j) = f32x4{0.f, 0.f, 0.f, 0.f};
+      return;
+    }
+  }
+  zero_tail<OutT>(orow, from, cols);
+}
+
+// One (token, group) row with the whole key block in LDS.  kOutQ = out_cols/64
+// is a compile-time count: the row is written by exactly kOutQ 64-column
+// stores (computed chunks, then zeros), so the number of memory operations
+// between one row's query prefetch and its use is known to the compiler and
+// the wait before the next row covers only what it must.
+template <typename OutT, int kOutQ>
+__device__ __forceinline__ void lds_row(const Stage1Args& a, const bf16x8* kt, const Segment& sg,
+                                        int64_t t, int32_t lq, const Frag& qf) {
+  const int lane = threadIdx.x & (kWave - 1);
+  OutT* orow = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + t) * a.out_cols;
+  int32_t vis = sg.lk;
+  if (a.causal) {
+    vis = tdiv16(lq - 15) + sg.lk - tdiv16(sg.lq_len - 16 + 1);
+    vis = vis < 0 ? 0 : (vis > sg.lk ? sg.lk : vis);
+  }
+  vis = vis < 64 * kOutQ ? vis : 64 * kOutQ;  // keys past the output row are not written
+  vis = __builtin_amdgcn_readfirstlane(vis);   // wave-uniform: scalar branches below
+  const int nq = (vis + 63) >> 6;              // 64-key quads; 0 when nothing is visible
+  const float c = a.scale_log2;                // > 0 on this path
+  const bf16x8* kl = kt + lane;
+
+  // Scores of a quad (four 16-key tiles): the four tiles' accumulation chains
+  // are interleaved over the four K = 32 steps, and the next step's four
+  // B fragments are read from LDS while the current step's MFMAs run.
+  f32x4 s[4 * kOutQ];
+#pragma unroll
+  for (int qd = 0; qd < kOutQ; ++qd) {
+    if (qd < nq) {
+      const bf16x8* kq = kl + qd * 16 * kWave;  // fragment (u, cc) at kq[(4u + cc) * 64]
+      f32x4 acc[4];
+      bf16x8 cur[4], nxt[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        cur[u] = kq[(4 * u + 0) * kWave];
+      }
+#pragma unroll
+      for (int cc = 0; cc < kD / 32; ++cc) {
+        if (cc + 1 < kD / 32) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) nxt[u] = kq[(4 * u + cc + 1) * kWave];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf.v[cc], cur[u], acc[u], 0, 0, 0);
+        if (cc + 1 < kD / 32) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s[4 * qd + u] = acc[u];
+    }
+  }
+  // Max over the visible raw scores (scale > 0 keeps the order).  Only the
+  // last computed quad holds keys >= vis, so only it is masked; masked scores
+  // are -inf and exponentiate to 0 below.
+  float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int qd = 0; qd < kOutQ; ++qd) {
+    if (qd < nq) {
+      if (qd == nq - 1) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool ok = 64 * qd + 16 * u + (lane & 15) < vis;
+          const int jt = 4 * qd + u;
+          s[jt].x = ok ? s[jt].x : -INFINITY;
+          s[jt].y = ok ? s[jt].y : -INFINITY;
+          s[jt].z = ok ? s[jt].z : -INFINITY;
+          s[jt].w = ok ? s[jt].w : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int jt = 4 * qd + u;
+        m[0] = fmaxf(m[0], s[jt].x);
+        m[1] = fmaxf(m[1], s[jt].y);
+        m[2] = fmaxf(m[2], s[jt].z);
+        m[3] = fmaxf(m[3], s[jt].w);
+      }
+    }
+  }
+  // p = exp2(c*s - c*max): one fma and one exp per score.
+  float mc[4], l[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mc[r] = -c * grp_max16(m[r]);
+    l[r] = 0.f;
+  }
+#pragma unroll
+  for (int qd = 0; qd < kOutQ; ++qd) {
+    if (qd < nq) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int jt = 4 * qd + u;
+        s[jt].x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].x, c, mc[0]));
+        s[jt].y = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].y, c, mc[1]));
+        s[jt].z = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].z, c, mc[2]));
+        s[jt].w = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].w, c, mc[3]));
+        l[0] += s[jt].x;
+        l[1] += s[jt].y;
+        l[2] += s[jt].z;
+        l[3] += s[jt].w;
+      }
+    }
+  }
+  // Normalise and sum over the 16 heads on the matrix core: for tiles u of a
+  // quad, B = the tile's exponentials as f16 (lane (key n, group g) holds
+  // heads 4g..4g+3 -- the accumulator layout of the score MFMA is the B
+  // layout with heads as the reduction index), A = 1/l of those heads placed
+  // on rows 4u..4u+3.  Two K = 32 MFMAs (tiles 0,1 then 2,3, accumulated)
+  // leave every lane of group u holding the output of tile u for key l%16,
+  // i.e. the quad's 64 outputs in lane order.
+  f16x8 wa, wb;  // A operands: tiles (0,1) and (2,3)
+  {
+    float inv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv[r] = __builtin_amdgcn_rcpf(grp_sum16(l[r]));
+    const int m = lane & 15;  // A row of this lane
+    const _Float16 h0 = static_cast<_Float16>(inv[0]), h1 = static_cast<_Float16>(inv[1]);
+    const _Float16 h2 = static_cast<_Float16>(inv[2]), h3 = static_cast<_Float16>(inv[3]);
+    const _Float16 z = static_cast<_Float16>(0.f);
+    const bool lo_a = m < 4, hi_a = m >= 4 && m < 8, lo_b = m >= 8 && m < 12, hi_b = m >= 12;
+    wa = f16x8{lo_a ? h0 : z, lo_a ? h1 : z, lo_a ? h2 : z, lo_a ? h3 : z,
+               hi_a ? h0 : z, hi_a ? h1 : z, hi_a ? h2 : z, hi_a ? h3 : z};
+    wb = f16x8{lo_b ? h0 : z, lo_b ? h1 : z, lo_b ? h2 : z, lo_b ? h3 : z,
+               hi_b ? h0 : z, hi_b ? h1 : z, hi_b ? h2 : z, hi_b ? h3 : z};
+  }
+#pragma unroll
+  for (int qd = 0; qd < kOutQ; ++qd) {
+    float o = 0.f;
+    if (qd < nq) {
+      const f32x4* e = s + 4 * qd;
+      const f16x8 b01 = f16x8{static_cast<_Float16>(e[0].x), static_cast<_Float16>(e[0].y),
+                              static_cast<_Float16>(e[0].z), static_cast<_Float16>(e[0].w),
+                              static_cast<_Float16>(e[1].x), static_cast<_Float16>(e[1].y),
+                              static_cast<_Float16>(e[1].z), static_cast<_Float16>(e[1].w)};
+      const f16x8 b23 = f16x8{static_cast<_Float16>(e[2].x), static_cast<_Float16>(e[2].y),
+                              static_cast<_Float16>(e[2].z), static_cast<_Float16>(e[2].w),
+                              static_cast<_Float16>(e[3].x), static_cast<_Float16>(e[3].y),
+                              static_cast<_Float16>(e[3].z), static_cast<_Float16>(e[3].w)};
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, acc, 0, 0, 0);
+      o = acc.x;
+    }
+    store_out<OutT>(orow + 64 * qd + lane, o);
+  }
+}
+
+template <typename OutT, int kOutQ>
+__global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
+  __shared__ bf16x8 kt[kLdsUnits];
+  const int wave = threadIdx.x >> 6;
+  const int64_t r_begin = n_rows * blockIdx.x / gridDim.x;
+  const int64_t r_end = n_rows * (blockIdx.x + 1) / gridDim.x;
+  for (int64_t r = r_begin; r < r_end;) {
+    const Segment sg = find_segment(a, r, r_end);
+    const int64_t n = sg.end - r;
+    __syncthreads();  // the previous segment is done with kt
+    if (sg.kind == kSeq && sg.lk > 0) {
+      int ntl = 4 * ((sg.lk + 63) >> 6);
+      ntl = ntl < 4 * kOutQ ? ntl : 4 * kOutQ;
+      load_k_block(a, kt, sg, ntl);
+    }
+    __syncthreads();
+    // Wave w takes the row pairs (2w, 2w+1), (2w+16, 2w+17), ... of the
+    // segment: in zig-zag order each pair is one short and one long causal
+    // row, so the waves get equal work without a shared counter.
+    auto my_row = [&](int64_t j) -> int64_t { return (j >> 1) * (2 * kLdsWaves) + 2 * wave + (j & 1); };
+    if (sg.kind == kOrphan) {
+      for (int64_t j = 0; my_row(j) < n; ++j) {
+        const int64_t rel = r + my_row(j) - sg.rlo;
+        const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
+        if (g < a.Hkv && t < a.Tq)
+          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+      }
+    } else if (sg.kind == kSeq && my_row(0) < n) {
+      int32_t lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(0), sg.lq_len));
+      Frag qn = load_q_frag(a, sg.qs + lq_n, sg.g);
+      for (int64_t j = 0; my_row(j) < n; ++j) {
+        const Frag qf = qn;
+        const int32_t lq = lq_n;
+        // Prefetch the next row's query (the current one again past the end,
+        // so every iteration issues the same loads).
+        const int64_t i2 = my_row(j + 1) < n ? my_row(j + 1) : my_row(j);
+        lq_n = static_cast<int32_t>(zigzag(sg.k0 + i2, sg.lq_len));
+        qn = load_q_frag(a, sg.qs + lq_n, sg.g);
+        lds_row<OutT, kOutQ>(a, kt, sg, sg.qs + lq, lq, qf);
+      }
+    }
+    r = sg.end;
+  }
+}
+
+int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <typename OutT>
 int launch_stage1(const Stage1Args& a, hipStream_t s) {
   const bool aligned = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 && (a.q_st % 8) == 0 &&
                        (a.q_sh % 8) == 0 && (a.k_st % 8) == 0 && (a.k_sh % 8) == 0;
-  if (a.G == kG && a.D == kD && aligned) {
+  if (a.G == kG && a.D == kD && aligned && a.out_cols <= kLdsTiles * 16 &&
+      (a.out_cols % 64) == 0 && a.scale_log2 > 0.f) {
+    const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
+    int64_t grid = (n_rows + kLdsWaves - 1) / kLdsWaves;
+    const int64_t cus = num_cus();
+    grid = grid < cus ? grid : cus;
+    const dim3 g(static_cast<unsigned>(grid)), b(kLdsWaves * kWave);
+    switch (a.out_cols / 64) {
+      case 1: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 1>), g, b, 0, s, a, n_rows); break;
+      case 2: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 2>), g, b, 0, s, a, n_rows); break;
+      case 3: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 3>), g, b, 0, s, a, n_rows); break;
+      case 4: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 4>), g, b, 0, s, a, n_rows); break;
+      case 5: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 5>), g, b, 0, s, a, n_rows); break;
+      case 6: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 6>), g, b, 0, s, a, n_rows); break;
+      case 7: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 7>), g, b, 0, s, a, n_rows); break;
+      default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
+    }
+  } else if (a.G == kG && a.D == kD && aligned) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
     hipLaunchKernelGGL(stage1_mfma_kernel<OutT>, grid, dim3(256), 0, s, a);
   } else {
