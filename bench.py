@@ -39,8 +39,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (e.g. under a profiler)")
-    ap.add_argument("--only", choices=["stage1", "maxpool", "block_table"], default=None,
-                    help="run a single kernel (profiling)")
+    ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "copy"], default=None,
+                    help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
+                         "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -96,6 +97,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only == "copy":
+        calibration_copy(dev, args)
+        return
     s1, s1g, mp, mpg, bt = build_inputs(dev)
     mp_kw = {k: mp[k] for k in ("max_seqlen_q", "max_context_len", "local_blocks",
                                 "init_blocks", "block_size", "stride")}
@@ -123,20 +127,31 @@ def main():
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
 
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in ops] for _ in range(args.steps)]
+    # The timed region: K steps of the path (stage 1, max-pool, block table),
+    # bracketed by device synchronisation; its wall clock gives ms_per_step.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(args.steps):
-        for i, (_, fn) in enumerate(ops):
-            ev[s][i][0].record()
+    for _ in range(args.steps):
+        for _, fn in ops:
             fn()
-            ev[s][i][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_op = {name: sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps))
-              / args.steps for i, (name, _) in enumerate(ops)}          # ms
-    log("timed: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in per_op.items()))
+
+    # Per-kernel launch durations: K back-to-back launches of one kernel
+    # between two HIP events on torch's current stream (the stream the
+    # kernels run on), so per-launch event overhead is amortised.
+    per_op = {}
+    for name, fn in ops:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        fn()
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per_op[name] = e0.elapsed_time(e1) / args.steps          # ms
+    log("per-kernel: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in per_op.items())
+        + f"; step {wall * 1e3 / args.steps:.3f} ms")
 
     comps = {}
     if "stage1" in per_op:
@@ -197,6 +212,20 @@ def main():
                             "mfma_frac": round(s1c["tflops"] / PEAK_BF16_TFLOPS, 4)}
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
+
+
+def calibration_copy(dev, args):
+    """A plain 256 MiB device-to-device copy (reads and writes exactly 256 MiB):
+    what FETCH_SIZE / WRITE_SIZE report for it scales the kernels' readings."""
+    import torch
+
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup + args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n}), flush=True)
 
 
 def cpu_baseline(s1):

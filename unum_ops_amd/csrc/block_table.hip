@@ -10,8 +10,8 @@
 // time, one per lane, and broadcast with a lane shuffle; each store step
 // writes four whole runs (1 KiB, one dwordx4 per lane).  The block-table
 // gather for those entries is one dwordx4 load when the four positions are
-// valid, in range and 16-byte aligned.  The kernel is bound by the output
-// write.
+// valid, in range and 16-byte aligned, issued eight steps ahead of use.  The
+// kernel is bound by the output write.
 #include "common.h"
 
 namespace unum {
@@ -91,21 +91,25 @@ __global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a) {
   for (int32_t kb = 0; kb < a.K; kb += kWave) {
     const int32_t my = (kb + lane < a.K) ? ids[static_cast<int64_t>(kb + lane) * a.s_k] : -1;
     if (kVecTable && a.K - kb >= kWave) {
-      // Sixteen store steps of four runs each; all table loads go out first.
-      int32_t p0[16];
-      i32x4 raw[16];
+      // Sixteen store steps of four runs each, in two batches of eight whose
+      // table loads all go out before the first is used.
 #pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const int32_t idx = __shfl(my, 4 * st + sub);
-        p0[st] = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
-        const int32_t safe = (p0[st] >= 0 && p0[st] <= vec_hi) ? p0[st] : 0;
-        raw[st] = *reinterpret_cast<const i32x4*>(row + safe);
-      }
+      for (int half = 0; half < 2; ++half) {
+        int32_t p0[8];
+        i32x4 raw[8];
 #pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const bool raw_ok = p0[st] >= 0 && p0[st] <= vec_hi;
-        out[static_cast<int64_t>(kb + 4 * st + sub) * 16 + (lane & 15)] =
-            finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h);
+        for (int st = 0; st < 8; ++st) {
+          const int32_t idx = __shfl(my, 4 * (8 * half + st) + sub);
+          p0[st] = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
+          const int32_t safe = (p0[st] >= 0 && p0[st] <= vec_hi) ? p0[st] : 0;
+          raw[st] = *reinterpret_cast<const i32x4*>(row + safe);
+        }
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+          const bool raw_ok = p0[st] >= 0 && p0[st] <= vec_hi;
+          out[static_cast<int64_t>(kb + 4 * (8 * half + st) + sub) * 16 + (lane & 15)] =
+              finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h);
+        }
       }
     } else {
       const int32_t steps = (a.K - kb) < kWave ? (a.K - kb + 3) / 4 : kWave / 4;

@@ -3,15 +3,17 @@
 // Reference semantics: the Triton kernel _max_pooling_1d_varlen_kernel and its
 // wrapper (src/unum_ops/infllm_v2/max_pooling_1d_varlen.py:33-183).
 //
-// Work decomposition: one wave owns a 256-output chunk of one row (h, t) and
-// walks it in four steps of 64 outputs, one output n per lane.  With the
+// Work decomposition: one wave owns one (row, 256-output chunk) unit; lane i
+// owns four consecutive outputs n0..n0+3 (n0 = 256*chunk + 4i).  With the
 // reference's block_size 64 / stride 16 (P = 4 taps per step, 5-tap windows,
-// padding 1) window n covers taps 4n-1 .. 4n+3: the lane reads taps 4n..4n+3
-// as one vector -- a wave's load is one contiguous 1 KiB (fp32) -- and takes
-// tap 4n-1 from the lane below (lane 0 from the previous step).  Every input
-// element is read from HBM once and every output written once, so the kernel
-// is bound by HBM bandwidth.  The row -> sequence lookup is one 64-lane
-// vector load of cu_seqlens_q and a ballot, done once per wave.
+// padding 1) their windows cover taps 4*n0-1 .. 4*n0+15: the lane reads the
+// sixteen taps 4*n0 .. 4*n0+15 as 16-byte vectors, takes tap 4*n0-1 from the
+// lane below (lane 0 reads it), and writes its four outputs with one 16-byte
+// store.  Every input element is read from HBM once and every output written
+// once, so the kernel is bound by HBM bandwidth; waves are kept light (about
+// 32 VGPRs) so many are resident, which measured faster than fewer waves
+// with deeper per-wave batches.  The row -> sequence lookup is one 64-lane
+// vector load of cu_seqlens_q and a ballot.
 #include "common.h"
 
 namespace unum {
@@ -76,111 +78,121 @@ __device__ __forceinline__ int find_sequence(const int32_t* cu_q, int64_t B, int
   return (t < cu_q[b + 1]) ? b : -1;
 }
 
+// Fast path: P == 4 (block_size / stride == 4).
 template <typename T>
-struct Vec4;
+struct Vec16;  // sixteen consecutive taps as fp32
 template <>
-struct Vec4<float> {
-  static __device__ __forceinline__ f32x4 load(const void* p, int64_t i) {
-    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
-  }
-};
-template <>
-struct Vec4<__bf16> {
-  static __device__ __forceinline__ f32x4 load(const void* p, int64_t i) {
-    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
-    return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
-                 __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
-  }
-};
-template <>
-struct Vec4<_Float16> {
-  static __device__ __forceinline__ f32x4 load(const void* p, int64_t i) {
-    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
-    return f32x4{f16_bits_to_f32(static_cast<uint16_t>(w.x & 0xffffu)),
-                 f16_bits_to_f32(static_cast<uint16_t>(w.x >> 16)),
-                 f16_bits_to_f32(static_cast<uint16_t>(w.y & 0xffffu)),
-                 f16_bits_to_f32(static_cast<uint16_t>(w.y >> 16))};
-  }
-};
-
-// Fast path: P == 4 (block_size / stride == 4).  A wave processes kUnits
-// consecutive (row, 256-output chunk) units; every input load of all units is
-// issued before the first one is used, so a wave keeps 16 KiB of reads in
-// flight.
-constexpr int kUnits = 4;
-
-template <typename T, bool kVec>
-__global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
-  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  const int64_t u0 = wave * kUnits;
-  if (u0 >= a.n_units) return;  // wave-uniform
-  const int lane = threadIdx.x & (kWave - 1);
-
-  f32x4 v[kUnits][4];
-  float carry[kUnits];
-  int64_t lk[kUnits], ob[kUnits], out_base[kUnits], nfirst[kUnits];
+struct Vec16<float> {
+  static __device__ __forceinline__ void load(const void* p, int64_t i, float* v) {
+    const f32x4* q = reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
 #pragma unroll
-  for (int i = 0; i < kUnits; ++i) {
-    const int64_t u = u0 + i < a.n_units ? u0 + i : a.n_units - 1;  // tail: redo the last unit
-    const int64_t row = u / a.n_chunks;  // h*Tq + t
-    const int64_t chunk = u - row * a.n_chunks;
-    const int64_t t = row % a.Tq;
-    const int b = find_sequence(a.cu_q, a.B, t);
-    lk[i] = 0;
-    ob[i] = 0;
-    if (b >= 0) {
-      lk[i] = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
-      ob[i] = (t - a.cu_q[b]) / a.block_size;
+    for (int k = 0; k < 4; ++k) {
+      const f32x4 w = q[k];
+      v[4 * k] = w.x; v[4 * k + 1] = w.y; v[4 * k + 2] = w.z; v[4 * k + 3] = w.w;
     }
-    const int64_t base = row * a.F;
-    // Taps are present below the key length, inside the input, and below the
-    // last tap any output window uses (4*NB - 1).
-    int64_t lim = lk[i] < (a.numel - base) ? lk[i] : (a.numel - base);
-    lim = lim < 4 * a.NB ? lim : 4 * a.NB;
-    nfirst[i] = chunk * 256;
-    out_base[i] = row * a.NB;
-    const int64_t p_first = 4 * nfirst[i];
-    {
-      const int64_t p = p_first - 1;
-      carry[i] = (p >= 0 && p < lim) ? Elem<T>::load(a.in, base + p) : -INFINITY;
-    }
-    if (kVec && p_first + 1023 < lim) {  // the whole chunk is present: plain vector loads
+  }
+};
+template <typename H, bool kBf16>
+struct Vec16Half {
+  static __device__ __forceinline__ void load(const void* p, int64_t i, float* v) {
+    const i32x4* q = reinterpret_cast<const i32x4*>(static_cast<const uint16_t*>(p) + i);
 #pragma unroll
-      for (int st = 0; st < 4; ++st) v[i][st] = Vec4<T>::load(a.in, base + p_first + 256 * st + 4 * lane);
-    } else {
+    for (int k = 0; k < 2; ++k) {
+      const i32x4 w = q[k];
+      const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int64_t p0 = p_first + 256 * st + 4 * lane;
-        if (kVec && p0 + 3 < lim) {
-          v[i][st] = Vec4<T>::load(a.in, base + p0);
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (kBf16) {
+          v[8 * k + 2 * e] = __uint_as_float(u[e] << 16);
+          v[8 * k + 2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
         } else {
-          v[i][st].x = (p0 + 0 < lim) ? Elem<T>::load(a.in, base + p0 + 0) : -INFINITY;
-          v[i][st].y = (p0 + 1 < lim) ? Elem<T>::load(a.in, base + p0 + 1) : -INFINITY;
-          v[i][st].z = (p0 + 2 < lim) ? Elem<T>::load(a.in, base + p0 + 2) : -INFINITY;
-          v[i][st].w = (p0 + 3 < lim) ? Elem<T>::load(a.in, base + p0 + 3) : -INFINITY;
+          v[8 * k + 2 * e] = f16_bits_to_f32(static_cast<uint16_t>(u[e] & 0xffffu));
+          v[8 * k + 2 * e + 1] = f16_bits_to_f32(static_cast<uint16_t>(u[e] >> 16));
         }
       }
     }
   }
+};
+template <>
+struct Vec16<__bf16> : Vec16Half<__bf16, true> {};
+template <>
+struct Vec16<_Float16> : Vec16Half<_Float16, false> {};
+
+template <typename T>
+__device__ __forceinline__ void store4(void* out, int64_t o, const float* r) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + o) = f32x4{r[0], r[1], r[2], r[3]};
+  } else {
+    uint16_t h[4];
 #pragma unroll
-  for (int i = 0; i < kUnits; ++i) {
-    if (u0 + i >= a.n_units) break;
-    float cy = carry[i];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const f32x4 w = v[i][st];
-      float prev = __shfl_up(w.w, 1);
-      prev = lane == 0 ? cy : prev;
-      cy = __shfl(w.w, kWave - 1);
-      const float m = fmaxf(fmaxf(fmaxf(prev, w.x), fmaxf(w.y, w.z)), w.w);
-      const int64_t n = nfirst[i] + 64 * st + lane;
-      const int64_t ws = 4 * n - 1;
-      const int64_t w_lo = ws < 0 ? 0 : ws;
-      const int64_t w_hi = (ws + 5) < lk[i] ? (ws + 5) : lk[i];
-      const bool force = n < a.init_blocks || (ob[i] >= n && ob[i] <= n + a.local_blocks);
-      const float r = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
-      if (n < a.NB) Elem<T>::store(a.out, out_base[i] + n, r);
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (__is_same(T, __bf16)) h[e] = f32_to_bf16_bits(r[e]);
+      else h[e] = f32_to_f16_bits(r[e]);
     }
+    uint2 pk;
+    pk.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    pk.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + o) = pk;
+  }
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
+  const int64_t u = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  if (u >= a.n_units) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = u / a.n_chunks;  // h*Tq + t
+  const int64_t chunk = u - row * a.n_chunks;
+  const int64_t t = row % a.Tq;
+
+  const int b = find_sequence(a.cu_q, a.B, t);
+  int64_t lk = 0, ob = 0;
+  if (b >= 0) {
+    lk = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
+    ob = (t - a.cu_q[b]) / a.block_size;
+  }
+  const int64_t base = row * a.F;
+  // Taps are present below the key length, inside the input, and below the
+  // last tap any output window uses (4*NB - 1).
+  int64_t lim = lk < (a.numel - base) ? lk : (a.numel - base);
+  lim = lim < 4 * a.NB ? lim : 4 * a.NB;
+
+  const int64_t n0 = chunk * 256 + 4 * lane;
+  const int64_t p0 = 4 * n0;
+  float v[16];
+  if (kVec && p0 + 15 < lim) {
+    Vec16<T>::load(a.in, base + p0, v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      v[j] = (p0 + j < lim) ? Elem<T>::load(a.in, base + p0 + j) : -INFINITY;
+  }
+  float prev = __shfl_up(v[15], 1);
+  if (lane == 0) {
+    const int64_t pe = p0 - 1;
+    prev = (pe >= 0 && pe < lim) ? Elem<T>::load(a.in, base + pe) : -INFINITY;
+  }
+  float r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t n = n0 + e;
+    const float first = e == 0 ? prev : v[4 * e - 1];
+    const float m = fmaxf(fmaxf(first, v[4 * e]),
+                          fmaxf(fmaxf(v[4 * e + 1], v[4 * e + 2]), v[4 * e + 3]));
+    const int64_t ws = 4 * n - 1;
+    const int64_t w_lo = ws < 0 ? 0 : ws;
+    const int64_t w_hi = (ws + 5) < lk ? (ws + 5) : lk;
+    const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
+    r[e] = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
+  }
+  const int64_t o = row * a.NB + n0;
+  if (n0 >= a.NB) return;
+  if (kVec && n0 + 3 < a.NB) {
+    store4<T>(a.out, o, r);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n0 + e < a.NB) Elem<T>::store(a.out, o + e, r[e]);
   }
 }
 
@@ -224,9 +236,12 @@ int launch_pool(const PoolArgs& a, hipStream_t s) {
   const int64_t blocks = (a.n_units * kWave + threads - 1) / threads;  // generic: one wave per unit
   if (blocks > INT32_MAX) UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen: too many rows");
   if (a.P == 4) {
-    const int64_t waves = (a.n_units + kUnits - 1) / kUnits;
-    const int64_t blocks4 = (waves * kWave + threads - 1) / threads;
-    const bool vec = (reinterpret_cast<uintptr_t>(a.in) & 15) == 0 && (a.F % 4) == 0;
+    const int64_t blocks4 = blocks;  // one wave per unit
+    // Vector loads need 16-byte aligned taps (F a multiple of 16 bytes' worth of
+    // elements), vector stores 16/8-byte aligned output runs (NB % 4 == 0).
+    const bool vec = (reinterpret_cast<uintptr_t>(a.in) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+                     ((a.F * (int64_t)sizeof(T)) % 16) == 0 && (a.NB % 4) == 0;
     if (vec)
       hipLaunchKernelGGL((maxpool_p4_kernel<T, true>), dim3((unsigned)blocks4), dim3(threads), 0, s, a);
     else
