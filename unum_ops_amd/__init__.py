@@ -14,8 +14,8 @@ runs hand-written HIP kernels through the C ABI in ``include/unum_ops_amd.h``.
 
 import torch  # noqa: F401  -- load torch's HIP runtime before the native library
 
-from . import infllm_v2, sparse_kernel_extension  # noqa: E402
+from . import infllm_v2, pipeline, sparse_kernel_extension  # noqa: E402
 
 __version__ = "0.1.0"
 
-__all__ = ["infllm_v2", "sparse_kernel_extension", "__version__"]
+__all__ = ["infllm_v2", "pipeline", "sparse_kernel_extension", "__version__"]
