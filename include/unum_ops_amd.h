@@ -67,7 +67,9 @@ int unum_abi_version(void);
  *   out[g, t, j] = sum_{i<G} softmax_j(scale * q[t, gG+i] . k[cu_k[b]+j, g])
  * over the visible keys j < vis(t) (causal rule of the reference, truncating
  * division), 0 for vis <= j < out_cols, and 0 for the whole row when
- * vis == 0 or the sequence has no keys.  Every element of `out` is written.
+ * vis == 0 or the sequence has no keys.  Every element of `out` is written;
+ * keys of a sequence at j >= out_cols are not (the reference writes past the
+ * row there).
  *
  * `workspace` must hold unum_infllmv2_attn_stage1_workspace_size(...) bytes
  * (it may be NULL when that size is 0).

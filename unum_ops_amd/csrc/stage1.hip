@@ -399,8 +399,9 @@ __global__ __launch_bounds__(64) void stage1_generic_kernel(Stage1Args a) {
 // touches one or two (sequence, group) K blocks -- loaded once -- and its
 // causal work (which grows linearly with the token position) is balanced,
 // since consecutive zig-zag rows pair a short prefix with a long one.  Inside
-// a workgroup, waves take rows from an LDS counter and prefetch the next
-// row's query fragment while computing the current one.
+// a workgroup, wave w takes the row pairs (2w, 2w+1), (2w+16, 2w+17), ... of
+// a segment and prefetches the next row's query fragment while computing the
+// current one.
 constexpr int kLdsWaves = 8;
 constexpr int kLdsTiles = 32;                    // 512 keys
 constexpr int kLdsUnits = kLdsTiles * 4 * kWave; // bf16x8 units: 128 KiB
