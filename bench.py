@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (e.g. under a profiler)")
-    ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "copy"], default=None,
+    ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
+                                       "maxpool_cfg5", "copy"], default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -76,10 +77,16 @@ def build_inputs(dev):
     bt = dict(topk_idx=topk, block_table=p5["block_table"].to(dev),
               token_to_bs=p5["token_to_bs"].to(dev), token_pos_in_bs=p5["token_pos_in_bs"].to(dev),
               seqlen_q=p5["seqlen_q"].to(dev))
-    del sc, pooled, q5, k5
+    # cfg5's stage 1 and max-pool are timed too (reported as components, not
+    # part of the headline step).
+    c5 = dict(q=q5, k=k5, cu_q=cu_q5, cu_k=cu_k5, max_seqlen_k=p5["max_seqlen_k"],
+              max_context_len=p5["max_context_len"], scores=sc,
+              cache=torch.zeros(1, dtype=torch.int32, device=dev),
+              cu_q_cpu=p5["cu_seqlens_q"], cu_k_cpu=p5["cu_seqlens_k"])
+    del pooled
     torch.cuda.synchronize()
-    log(f"cfg5 block-table inputs ready ({time.time() - t0:.1f}s)")
-    return s1, s1g, mp, mpg, bt
+    log(f"cfg5 inputs ready ({time.time() - t0:.1f}s)")
+    return s1, s1g, mp, mpg, bt, c5
 
 
 def main():
@@ -101,7 +108,7 @@ def main():
     if args.only == "copy":
         calibration_copy(dev, args)
         return
-    s1, s1g, mp, mpg, bt = build_inputs(dev)
+    s1, s1g, mp, mpg, bt, c5 = build_inputs(dev)
     mp_kw = {k: mp[k] for k in ("max_seqlen_q", "max_context_len", "local_blocks",
                                 "init_blocks", "block_size", "stride")}
 
@@ -118,9 +125,22 @@ def main():
         return get_block_table(bt["topk_idx"], bt["block_table"], bt["token_to_bs"],
                                bt["token_pos_in_bs"], bt["seqlen_q"])
 
+    def op_stage1_cfg5():
+        return infllmv2_attn_stage1(c5["q"], c5["k"], None, c5["cu_q"], c5["cu_k"],
+                                    max_seqlen_k=c5["max_seqlen_k"], causal=True)
+
+    def op_maxpool_cfg5():
+        return max_pooling_1d_varlen(c5["scores"], c5["cu_q"], c5["cu_k"], c5["cache"],
+                                     max_seqlen_q=16 * c5["scores"].shape[-1],
+                                     max_context_len=c5["max_context_len"], local_blocks=1,
+                                     init_blocks=1)
+
     ops = [("stage1", op_stage1), ("maxpool", op_maxpool), ("block_table", op_block_table)]
+    # Timed per kernel only: the long-context configuration's stage 1 and max-pool.
+    extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
+        extra = [o for o in extra if o[0] == args.only]
 
     for _ in range(args.warmup):
         for _, fn in ops:
@@ -142,7 +162,7 @@ def main():
     # between two HIP events on torch's current stream (the stream the
     # kernels run on), so per-launch event overhead is amortised.
     per_op = {}
-    for name, fn in ops:
+    for name, fn in ops + extra:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         fn()
         e0.record()
@@ -179,6 +199,26 @@ def main():
                                     pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
                                     bytes=nbytes,
                                     config="cfg5 block-table stage: T=4096 H=2 K=64 -> int32 [4096,2,4096]")
+
+    if "stage1_cfg5" in per_op:
+        flop, nbytes, _ = workloads.stage1_work(c5["cu_q_cpu"], c5["cu_k_cpu"], 32, 2, 128,
+                                                c5["scores"].shape[-1])
+        t = per_op["stage1_cfg5"] * 1e-3
+        comps["stage1_cfg5"] = dict(us=per_op["stage1_cfg5"] * 1e3, tflops=flop / t / 1e12,
+                                    pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                                    gbs=nbytes / t / 1e9,
+                                    pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                    flop=flop, bytes=nbytes, bound="mfma",
+                                    config="cfg5 4096-token chunk of a 135168-token context, "
+                                           "Hq32/Hkv2/D128, fp32 out [2,4096,8448]")
+    if "maxpool_cfg5" in per_op:
+        nbytes = workloads.maxpool_bytes(c5["cu_q_cpu"], c5["cu_k_cpu"], [0], 2,
+                                         -(-c5["max_context_len"] // 64))
+        t = per_op["maxpool_cfg5"] * 1e-3
+        comps["maxpool_cfg5"] = dict(us=per_op["maxpool_cfg5"] * 1e3, gbs=nbytes / t / 1e9,
+                                     pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                     bytes=nbytes,
+                                     config="cfg5 scores fp32 [2,4096,8448] -> [2,4096,2112]")
 
     cpu = None
     if not args.no_cpu_baseline and "stage1" in comps:

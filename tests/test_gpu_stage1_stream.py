@@ -1,0 +1,101 @@
+"""GPU parity of the K-streaming stage-1 kernel (rows longer than 512 compressed
+keys) against the fp32 oracle, at atol 1e-3 / rtol 1e-2.
+
+Cases aimed at the kernel's own structure: 16-token pieces that straddle
+sequence boundaries, tokens that see no key, chunks cut by the sequence end,
+tokens outside every sequence, bf16 output, strided queries, and scores that
+grow along the keys far enough to force the running reference maximum to
+move (the rare re-do path).
+"""
+
+import pytest
+import torch
+
+from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
+from unum_ops_amd import workloads
+from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 1e-2
+
+
+def _run_check(d, dev, causal=True, out_dtype=torch.float32, q=None):
+    qd = (d["q"] if q is None else q).to(dev)
+    out = infllmv2_attn_stage1(qd, d["k"].to(dev), None, d["cu_seqlens_q"].to(dev),
+                               d["cu_seqlens_k"].to(dev), max_seqlen_k=d["max_seqlen_k"],
+                               causal=causal, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    exp = oracle_stage1(d["q"], d["k"], None, d["cu_seqlens_q"], d["cu_seqlens_k"],
+                        max_seqlen_k=d["max_seqlen_k"], causal=causal)
+    assert out.shape == exp.shape and out.shape[-1] > 512
+    if out_dtype == torch.bfloat16:
+        torch.testing.assert_close(out.float().cpu(), exp.to(torch.bfloat16).float(),
+                                   atol=2e-3, rtol=2e-2)
+    else:
+        torch.testing.assert_close(out.cpu(), exp, atol=ATOL, rtol=RTOL)
+    return out
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_pieces_straddle_sequences(causal, dev):
+    d = workloads.stage1_inputs([5, 30, 1, 17, 9], [9000, 600, 3000, 700, 5000], seed=41)
+    _run_check(d, dev, causal)
+
+
+def test_tokens_without_visible_keys(dev):
+    # 1000 queries on 100 context tokens (5 compressed keys): the early tokens
+    # see nothing; the second sequence makes the rows long.
+    d = workloads.stage1_inputs([1000, 4], [100, 9000], seed=42)
+    out = _run_check(d, dev)
+    assert float(out[:, :40].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("ctx", [32 + 16 * 512, 32 + 16 * 513, 32 + 16 * 766])
+def test_chunk_boundaries(ctx, dev):
+    # compressed lengths 513 / 514 / 767: the last 256-key chunk is cut
+    d = workloads.stage1_inputs([20], [ctx], seed=ctx)
+    _run_check(d, dev)
+
+
+def test_tokens_outside_sequences(dev):
+    d = workloads.stage1_inputs([10, 20], [3000, 9000], seed=43)
+    q = torch.cat([torch.randn(3, 32, 128).to(torch.bfloat16), d["q"],
+                   torch.randn(6, 32, 128).to(torch.bfloat16)])
+    d["q"] = q
+    d["cu_seqlens_q"] = d["cu_seqlens_q"] + 3
+    out = _run_check(d, dev)
+    assert float(out[:, :3].abs().max()) == 0.0 and float(out[:, -6:].abs().max()) == 0.0
+
+
+def test_bf16_output(dev):
+    d = workloads.stage1_inputs([33, 7], [9000, 2000], seed=44)
+    _run_check(d, dev, out_dtype=torch.bfloat16)
+
+
+def test_strided_queries(dev):
+    d = workloads.stage1_inputs([24, 9], [6000, 9000], seed=45)
+    wide = torch.zeros(d["q"].shape[0], 48, 128, dtype=torch.bfloat16)
+    wide[:, 8:40] = d["q"]
+    _run_check(d, dev, q=wide[:, 8:40])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_growing_scores_move_the_reference(causal, dev):
+    # Scores rise linearly along the keys up to ~2000 (log2-domain ~260), far
+    # above the first quad's maximum: pass 1 must re-base its reference.
+    Lq, ctx = 40, 48032
+    Lk = workloads.compressed_len(ctx)
+    q = torch.ones(Lq, 32, 128).to(torch.bfloat16)
+    ramp = (torch.arange(Lk, dtype=torch.float32) / Lk * 16.0)
+    k = ramp[:, None, None].expand(Lk, 2, 128).contiguous().to(torch.bfloat16)
+    d = dict(q=q, k=k, cu_seqlens_q=torch.tensor([0, Lq], dtype=torch.int32),
+             cu_seqlens_k=torch.tensor([0, Lk], dtype=torch.int32), max_seqlen_k=Lk)
+    out = _run_check(d, dev, causal)
+    assert torch.isfinite(out).all()
+
+
+def test_large_magnitude_keys(dev):
+    d = workloads.stage1_inputs([50, 16], [20000, 7000], seed=46)
+    d["k"] = (d["k"].float() * 40.0).to(torch.bfloat16)
+    _run_check(d, dev)

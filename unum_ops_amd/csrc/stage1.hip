@@ -754,6 +754,362 @@ __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args
   }
 }
 
+// ------------------------------------------------------ K-streaming path
+// For rows longer than the LDS-resident path holds (Kp > 512: long contexts,
+// decode against a large cache).  A workgroup of eight waves owns a piece of
+// up to 8*TW consecutive tokens of one (sequence, group); wave w computes the
+// tokens w, w+8, ... (TW of them), so every K fragment read from LDS feeds TW
+// score MFMAs.  K streams through two 64 KiB LDS buffers in the fragment order
+// of the resident path, 256 keys at a time: the next chunk's loads are issued
+// into registers before the current chunk is computed and written to the free
+// buffer after it, with one barrier per chunk.
+//
+// The reference's two passes, with the VALU work per score kept to an fma, an
+// exp and one more op:
+//   pass 1: l += exp2(c*s - c*mref) per (lane, head), where mref is a per-lane
+//           reference taken from the first quad's exact max and moved only when
+//           a quad's sum of exponentials exceeds 2^64 (the quad is then redone
+//           against its exact max, so nothing overflows); the lanes' (mref, l)
+//           are combined at the end into bias = c*max + log2(sum);
+//   pass 2: p = exp2(c*s - bias) is already normalised; the sum over the 16
+//           heads runs on the matrix core (an f16 MFMA against a 0/1 pattern)
+//           and each 64-key quad is stored with one buffer store per token.
+// Every quad of a streamed chunk is computed (keys past the visible range are
+// masked to 0), and stores past the row are dropped by the buffer range check,
+// so each chunk issues the same memory operations and waits stay exact.
+constexpr int kStWaves = 8;
+constexpr int kStChunkTiles = 16;                          // 256 keys
+constexpr int kStChunkUnits = kStChunkTiles * 4 * kWave;   // 4096 bf16x8 units: 64 KiB
+constexpr int kStPer = kStChunkUnits / (kStWaves * kWave); // 8 loads per thread
+constexpr uint32_t kBufferFlags = 0x00020000;              // gfx9 raw buffer resource word 3
+constexpr float kStLimit = 18446744073709551616.f;         // 2^64
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           static_cast<int>(kBufferFlags));
+}
+
+// Issue the loads of chunk `ch` (keys 256*ch ..) of the piece's K block; keys
+// past the valid range read as zero (buffer range check).
+__device__ __forceinline__ void stream_issue(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int ch,
+                                             u32x4 (&v)[kStPer]) {
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+#pragma unroll
+  for (int i = 0; i < kStPer; ++i) {
+    const int u = tid + i * kStWaves * kWave;
+    const int jt = u >> 8, cc = (u >> 6) & 3, l = u & 63;
+    const int key = kStChunkTiles * 16 * ch + 16 * jt + (l & 15);
+    const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (l >> 4)) * 2);
+    v[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
+  }
+}
+__device__ __forceinline__ void stream_commit(bf16x8* buf, const u32x4 (&v)[kStPer]) {
+#pragma unroll
+  for (int i = 0; i < kStPer; ++i) {
+    const int u = static_cast<int>(threadIdx.x) + i * kStWaves * kWave;
+    buf[u] = __builtin_bit_cast(bf16x8, v[i]);
+  }
+}
+
+// Scores of quad qd (keys 64*qd .. +63 of the chunk in `buf`) for TW tokens.
+template <int TW>
+__device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const Frag (&qf)[TW],
+                                              f32x4 (&acc)[TW][4]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int qbase = qd * 16 * kWave + lane;
+  asm volatile("" : "+v"(qbase));
+  const bf16x8* kq = buf + qbase;  // fragment (u, cc) at kq[(4u + cc) * 64]
+  bf16x8 cur[4], nxt[4];
+#pragma unroll
+  for (int k = 0; k < TW; ++k)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[k][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 4; ++u) cur[u] = kq[(4 * u) * kWave];
+#pragma unroll
+  for (int cc = 0; cc < kD / 32; ++cc) {
+    if (cc + 1 < kD / 32) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) nxt[u] = kq[(4 * u + cc + 1) * kWave];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < TW; ++k)
+        acc[k][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[k].v[cc], cur[u], acc[k][u], 0, 0, 0);
+    if (cc + 1 < kD / 32) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+    }
+  }
+}
+
+template <typename OutT, int TW>
+__global__ __launch_bounds__(kStWaves* kWave) void stage1_stream_kernel(Stage1Args a, int64_t n_rows) {
+  __shared__ bf16x8 kbuf[2][kStChunkUnits];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & (kWave - 1);
+  const float c = a.scale_log2;  // > 0 on this path
+  constexpr int R = kStWaves * TW;
+  const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * R;
+  const int64_t r_end = r_begin + R < n_rows ? r_begin + R : n_rows;
+  // Head-sum pattern: A row m has ones at the k-slots of the heads of tile
+  // u = m/4 (tiles 0,1 in wa, tiles 2,3 in wb), so lane group u of the result
+  // holds tile u's per-key head sum.
+  f16x8 wa, wb;
+  {
+    const int m = lane & 15;
+    const _Float16 one = static_cast<_Float16>(1.f), z = static_cast<_Float16>(0.f);
+    const _Float16 a0 = m < 4 ? one : z, a1 = (m >= 4 && m < 8) ? one : z;
+    const _Float16 b0 = (m >= 8 && m < 12) ? one : z, b1 = m >= 12 ? one : z;
+    wa = f16x8{a0, a0, a0, a0, a1, a1, a1, a1};
+    wb = f16x8{b0, b0, b0, b0, b1, b1, b1, b1};
+  }
+  const uint32_t row_bytes = static_cast<uint32_t>(a.out_cols * sizeof(OutT));
+
+  for (int64_t r = r_begin; r < r_end;) {
+    const Segment sg = find_segment(a, r, r_end);
+    const int64_t n = sg.end - r;
+    if (sg.kind == kOrphan) {
+      for (int64_t j = wave; j < n; j += kStWaves) {
+        const int64_t rel = r + j - sg.rlo;
+        const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
+        if (g < a.Hkv && t < a.Tq)
+          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+      }
+      r = sg.end;
+      continue;
+    }
+    if (sg.kind != kSeq) {
+      r = sg.end;
+      continue;
+    }
+    // Piece: tokens lq = k0 .. k0+n-1 of sequence b, group g (n <= R).
+    int32_t lq[TW], vis[TW];
+    bool own[TW];
+    auto vis_of = [&](int32_t q) -> int32_t {
+      int32_t v = sg.lk;
+      if (a.causal) {
+        v = tdiv16(q - 15) + sg.lk - tdiv16(sg.lq_len - 16 + 1);
+        v = v < 0 ? 0 : (v > sg.lk ? sg.lk : v);
+      }
+      return v < a.out_cols ? v : static_cast<int32_t>(a.out_cols);
+    };
+    int32_t vis_min = INT32_MAX;
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+      const int64_t i = wave + static_cast<int64_t>(kStWaves) * k;
+      own[k] = i < n;
+      lq[k] = static_cast<int32_t>(sg.k0 + (own[k] ? i : n - 1));
+      vis[k] = vis_of(lq[k]);
+      vis_min = vis[k] < vis_min ? vis[k] : vis_min;
+    }
+    // Causal visibility grows with the token, so the piece's last token sees
+    // the most keys.
+    const int32_t kv_hi = vis_of(static_cast<int32_t>(sg.k0 + n - 1));
+    const int nch = (kv_hi + kStChunkTiles * 16 - 1) / (kStChunkTiles * 16);
+    Frag qf[TW];
+#pragma unroll
+    for (int k = 0; k < TW; ++k) qf[k] = load_q_frag(a, sg.qs + lq[k], sg.g);
+
+    // K block of (sequence, group): keys [0, keys_ok) are readable.
+    const int64_t keys_ok = sg.lk < a.Tk - sg.ks ? sg.lk : a.Tk - sg.ks;
+    const __bf16* kbase = a.k + static_cast<int64_t>(sg.ks) * a.k_st + static_cast<int64_t>(sg.g) * a.k_sh;
+    const uint32_t k_bytes = keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, k_bytes);
+
+    float nb[TW][4];  // pass-2 bias: p = exp2(c*s + nb)
+    for (int pass = 0; pass < 2 && nch > 0; ++pass) {
+      float mref[TW][4], mc[TW][4], l[TW][4];
+#pragma unroll
+      for (int k = 0; k < TW; ++k)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          mref[k][rr] = -INFINITY;
+          mc[k][rr] = 0.f;
+          l[k][rr] = 0.f;
+        }
+      OutT* orow[TW];
+      __amdgpu_buffer_rsrc_t orsrc[TW];
+#pragma unroll
+      for (int k = 0; k < TW; ++k) {
+        orow[k] = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k]) * a.out_cols;
+        orsrc[k] = make_rsrc(orow[k], own[k] ? row_bytes : 0u);
+      }
+      u32x4 stage[kStPer];
+      __syncthreads();  // the previous user of kbuf is done
+      stream_issue(kr, a.k_st, 0, stage);
+      stream_commit(kbuf[0], stage);
+      __syncthreads();
+      for (int ch = 0; ch < nch; ++ch) {
+        const bf16x8* buf = kbuf[ch & 1];
+        if (ch + 1 < nch) stream_issue(kr, a.k_st, ch + 1, stage);
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          f32x4 acc[TW][4];
+          stream_scores<TW>(buf, qd, qf, acc);
+          const int key0 = kStChunkTiles * 16 * ch + 64 * qd;  // first key of the quad
+          const bool masked = key0 + 64 > vis_min;              // wave-uniform
+          if (pass == 0) {
+            if (masked) {
+#pragma unroll
+              for (int k = 0; k < TW; ++k)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  const bool ok = key0 + 16 * u + (lane & 15) < vis[k];
+                  acc[k][u].x = ok ? acc[k][u].x : -INFINITY;
+                  acc[k][u].y = ok ? acc[k][u].y : -INFINITY;
+                  acc[k][u].z = ok ? acc[k][u].z : -INFINITY;
+                  acc[k][u].w = ok ? acc[k][u].w : -INFINITY;
+                }
+            }
+            if (ch == 0 && qd == 0) {  // the reference: the first quad's exact max
+#pragma unroll
+              for (int k = 0; k < TW; ++k) {
+                float q4[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) q4[rr] = -INFINITY;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  q4[0] = fmaxf(q4[0], acc[k][u].x);
+                  q4[1] = fmaxf(q4[1], acc[k][u].y);
+                  q4[2] = fmaxf(q4[2], acc[k][u].z);
+                  q4[3] = fmaxf(q4[3], acc[k][u].w);
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                  mref[k][rr] = q4[rr];
+                  mc[k][rr] = q4[rr] == -INFINITY ? 0.f : -c * q4[rr];
+                }
+              }
+            }
+            float le[TW][4];
+            bool big = false;
+#pragma unroll
+            for (int k = 0; k < TW; ++k) {
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) le[k][rr] = 0.f;
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                le[k][0] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].x, c, mc[k][0]));
+                le[k][1] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].y, c, mc[k][1]));
+                le[k][2] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].z, c, mc[k][2]));
+                le[k][3] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].w, c, mc[k][3]));
+              }
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) big |= !(le[k][rr] <= kStLimit);
+            }
+            if (__builtin_amdgcn_ballot_w64(big) != 0) {
+              // Rare: a quad far above the reference.  Move the reference of
+              // the affected (lane, head) to the quad's exact max and redo it.
+#pragma unroll
+              for (int k = 0; k < TW; ++k) {
+                float q4[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) q4[rr] = -INFINITY;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  q4[0] = fmaxf(q4[0], acc[k][u].x);
+                  q4[1] = fmaxf(q4[1], acc[k][u].y);
+                  q4[2] = fmaxf(q4[2], acc[k][u].z);
+                  q4[3] = fmaxf(q4[3], acc[k][u].w);
+                }
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                  if (!(le[k][rr] <= kStLimit)) {
+                    const float nm = fmaxf(mref[k][rr], q4[rr]);
+                    l[k][rr] *= __builtin_amdgcn_exp2f((mref[k][rr] - nm) * c);
+                    mref[k][rr] = nm;
+                    mc[k][rr] = -c * nm;
+                    float e = 0.f;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                      const float sv = rr == 0 ? acc[k][u].x : rr == 1 ? acc[k][u].y
+                                     : rr == 2 ? acc[k][u].z : acc[k][u].w;
+                      e += __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, mc[k][rr]));
+                    }
+                    le[k][rr] = e;
+                  }
+                }
+              }
+            }
+#pragma unroll
+            for (int k = 0; k < TW; ++k)
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) l[k][rr] += le[k][rr];
+          } else {
+#pragma unroll
+            for (int k = 0; k < TW; ++k) {
+              f32x4 p[4];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                p[u].x = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].x, c, nb[k][0]));
+                p[u].y = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].y, c, nb[k][1]));
+                p[u].z = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].z, c, nb[k][2]));
+                p[u].w = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].w, c, nb[k][3]));
+              }
+              if (masked) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  const bool ok = key0 + 16 * u + (lane & 15) < vis[k];
+                  p[u].x = ok ? p[u].x : 0.f;
+                  p[u].y = ok ? p[u].y : 0.f;
+                  p[u].z = ok ? p[u].z : 0.f;
+                  p[u].w = ok ? p[u].w : 0.f;
+                }
+              }
+              const f16x8 b01 = f16x8{static_cast<_Float16>(p[0].x), static_cast<_Float16>(p[0].y),
+                                      static_cast<_Float16>(p[0].z), static_cast<_Float16>(p[0].w),
+                                      static_cast<_Float16>(p[1].x), static_cast<_Float16>(p[1].y),
+                                      static_cast<_Float16>(p[1].z), static_cast<_Float16>(p[1].w)};
+              const f16x8 b23 = f16x8{static_cast<_Float16>(p[2].x), static_cast<_Float16>(p[2].y),
+                                      static_cast<_Float16>(p[2].z), static_cast<_Float16>(p[2].w),
+                                      static_cast<_Float16>(p[3].x), static_cast<_Float16>(p[3].y),
+                                      static_cast<_Float16>(p[3].z), static_cast<_Float16>(p[3].w)};
+              f32x4 o = {0.f, 0.f, 0.f, 0.f};
+              o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, o, 0, 0, 0);
+              o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, o, 0, 0, 0);
+              const int off = (key0 + lane) * static_cast<int>(sizeof(OutT));
+              if constexpr (sizeof(OutT) == 4) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o.x), orsrc[k], off, 0, 0);
+              } else {
+                __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(o.x), orsrc[k], off, 0, 0);
+              }
+            }
+          }
+        }
+        if (ch + 1 < nch) stream_commit(kbuf[(ch + 1) & 1], stage);
+        __syncthreads();
+      }
+      if (pass == 0) {
+        // Combine the lanes' (reference, sum) into the row bias.
+#pragma unroll
+        for (int k = 0; k < TW; ++k)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const float M = grp_max16(mref[k][rr]);
+            const float part = mref[k][rr] == -INFINITY ? 0.f
+                               : l[k][rr] * __builtin_amdgcn_exp2f((mref[k][rr] - M) * c);
+            const float L = grp_sum16(part);
+            nb[k][rr] = L > 0.f ? -(M * c + __builtin_amdgcn_logf(L)) : -INFINITY;
+          }
+      }
+    }
+    // Columns past the streamed chunks.
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+      if (own[k]) {
+        OutT* orow = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k]) * a.out_cols;
+        zero_row_vec<OutT>(orow, static_cast<int64_t>(nch) * kStChunkTiles * 16, a.out_cols);
+      }
+    }
+    r = sg.end;
+  }
+}
+
 int num_cus() {
   static int cached[64] = {0};
   int dev = 0;
@@ -789,6 +1145,14 @@ int launch_stage1(const Stage1Args& a, hipStream_t s) {
       case 7: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 7>), g, b, 0, s, a, n_rows); break;
       default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
     }
+  } else if (a.G == kG && a.D == kD && aligned && a.scale_log2 > 0.f && a.k_st >= kD &&
+             (a.out_cols + kStChunkTiles * 16) * a.k_st * 2 < (int64_t{1} << 31) &&
+             a.out_cols * static_cast<int64_t>(sizeof(OutT)) < (int64_t{1} << 31)) {
+    constexpr int kTW = 2;
+    const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
+    const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kTW>), dim3(static_cast<unsigned>(grid)),
+                       dim3(kStWaves * kWave), 0, s, a, n_rows);
   } else if (a.G == kG && a.D == kD && aligned) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
     hipLaunchKernelGGL(stage1_mfma_kernel<OutT>, grid, dim3(256), 0, s, a);
