@@ -21,8 +21,8 @@ LIB_NAME = "libunum_ops_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = "gfx950"
 
-# Packed fp32 VALU ops are disabled for all device code (see the build notes
-# in the package README section of the design document).
+# Packed fp32 VALU ops (v_pk_*_f32) are disabled for all device code: some of
+# their forms have given wrong results on this hardware without any error.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -33,6 +33,14 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),
 ]
+
+# Extra flags per source.  Stage 1 never produces or consumes a NaN (masked
+# scores are -inf and every exp argument is finite or -inf), so it is built
+# without NaN semantics: fmaxf then needs no quieting and the DPP lane moves
+# fold into the max/add of the cross-lane reductions.
+FILE_FLAGS = {
+    "stage1.hip": ["-fno-honor-nans"],
+}
 
 
 def _hipcc():
@@ -65,7 +73,8 @@ def build(verbose=True, jobs=None):
 
     def compile_one(pair):
         src, obj = pair
-        return _run([hipcc, *HIP_FLAGS, "-c", src, "-o", obj])
+        extra = FILE_FLAGS.get(os.path.basename(src), [])
+        return _run([hipcc, *HIP_FLAGS, *extra, "-c", src, "-o", obj])
 
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:

@@ -712,7 +712,7 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, const bf16x8* kt, c
 template <typename OutT, int kOutQ>
 __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
   __shared__ bf16x8 kt[kLdsUnits];
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t r_begin = n_rows * blockIdx.x / gridDim.x;
   const int64_t r_end = n_rows * (blockIdx.x + 1) / gridDim.x;
   for (int64_t r = r_begin; r < r_end;) {
@@ -777,12 +777,18 @@ __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args
 // Every quad of a streamed chunk is computed (keys past the visible range are
 // masked to 0), and stores past the row are dropped by the buffer range check,
 // so each chunk issues the same memory operations and waits stay exact.
-constexpr int kStWaves = 8;
 constexpr int kStChunkTiles = 16;                          // 256 keys
 constexpr int kStChunkUnits = kStChunkTiles * 4 * kWave;   // 4096 bf16x8 units: 64 KiB
-constexpr int kStPer = kStChunkUnits / (kStWaves * kWave); // 8 loads per thread
 constexpr uint32_t kBufferFlags = 0x00020000;              // gfx9 raw buffer resource word 3
 constexpr float kStLimit = 18446744073709551616.f;         // 2^64
+#ifndef UNUM_STREAM_TW
+#define UNUM_STREAM_TW 2
+#endif
+#ifndef UNUM_STREAM_WAVES
+#define UNUM_STREAM_WAVES 8
+#endif
+constexpr int kStTokensPerWave = UNUM_STREAM_TW;  // tokens sharing each K fragment
+constexpr int kStWaves = UNUM_STREAM_WAVES;       // waves per workgroup
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -793,23 +799,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 // Issue the loads of chunk `ch` (keys 256*ch ..) of the piece's K block; keys
 // past the valid range read as zero (buffer range check).
+template <int W>
 __device__ __forceinline__ void stream_issue(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int ch,
-                                             u32x4 (&v)[kStPer]) {
+                                             u32x4 (&v)[kStChunkUnits / (W * kWave)]) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
 #pragma unroll
-  for (int i = 0; i < kStPer; ++i) {
-    const int u = tid + i * kStWaves * kWave;
+  for (int i = 0; i < kStChunkUnits / (W * kWave); ++i) {
+    const int u = tid + i * W * kWave;
     const int jt = u >> 8, cc = (u >> 6) & 3, l = u & 63;
     const int key = kStChunkTiles * 16 * ch + 16 * jt + (l & 15);
     const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (l >> 4)) * 2);
     v[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
   }
 }
-__device__ __forceinline__ void stream_commit(bf16x8* buf, const u32x4 (&v)[kStPer]) {
+template <int W>
+__device__ __forceinline__ void stream_commit(bf16x8* buf, const u32x4 (&v)[kStChunkUnits / (W * kWave)]) {
 #pragma unroll
-  for (int i = 0; i < kStPer; ++i) {
-    const int u = static_cast<int>(threadIdx.x) + i * kStWaves * kWave;
+  for (int i = 0; i < kStChunkUnits / (W * kWave); ++i) {
+    const int u = static_cast<int>(threadIdx.x) + i * W * kWave;
     buf[u] = __builtin_bit_cast(bf16x8, v[i]);
   }
 }
@@ -847,13 +855,16 @@ __device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const F
   }
 }
 
-template <typename OutT, int TW>
-__global__ __launch_bounds__(kStWaves* kWave) void stage1_stream_kernel(Stage1Args a, int64_t n_rows) {
+template <typename OutT, int W, int TW>
+__global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, int64_t n_rows) {
   __shared__ bf16x8 kbuf[2][kStChunkUnits];
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform by construction; readfirstlane lets the compiler keep the
+  // per-token rows and store descriptors in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & (kWave - 1);
   const float c = a.scale_log2;  // > 0 on this path
-  constexpr int R = kStWaves * TW;
+  constexpr int R = W * TW;
+  constexpr int kPer = kStChunkUnits / (W * kWave);
   const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * R;
   const int64_t r_end = r_begin + R < n_rows ? r_begin + R : n_rows;
   // Head-sum pattern: A row m has ones at the k-slots of the heads of tile
@@ -874,7 +885,7 @@ __global__ __launch_bounds__(kStWaves* kWave) void stage1_stream_kernel(Stage1Ar
     const Segment sg = find_segment(a, r, r_end);
     const int64_t n = sg.end - r;
     if (sg.kind == kOrphan) {
-      for (int64_t j = wave; j < n; j += kStWaves) {
+      for (int64_t j = wave; j < n; j += W) {
         const int64_t rel = r + j - sg.rlo;
         const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
         if (g < a.Hkv && t < a.Tq)
@@ -901,7 +912,7 @@ __global__ __launch_bounds__(kStWaves* kWave) void stage1_stream_kernel(Stage1Ar
     int32_t vis_min = INT32_MAX;
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
-      const int64_t i = wave + static_cast<int64_t>(kStWaves) * k;
+      const int64_t i = wave + static_cast<int64_t>(W) * k;
       own[k] = i < n;
       lq[k] = static_cast<int32_t>(sg.k0 + (own[k] ? i : n - 1));
       vis[k] = vis_of(lq[k]);
@@ -939,14 +950,14 @@ __global__ __launch_bounds__(kStWaves* kWave) void stage1_stream_kernel(Stage1Ar
         orow[k] = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k]) * a.out_cols;
         orsrc[k] = make_rsrc(orow[k], own[k] ? row_bytes : 0u);
       }
-      u32x4 stage[kStPer];
+      u32x4 stage[kPer];
       __syncthreads();  // the previous user of kbuf is done
-      stream_issue(kr, a.k_st, 0, stage);
-      stream_commit(kbuf[0], stage);
+      stream_issue<W>(kr, a.k_st, 0, stage);
+      stream_commit<W>(kbuf[0], stage);
       __syncthreads();
       for (int ch = 0; ch < nch; ++ch) {
         const bf16x8* buf = kbuf[ch & 1];
-        if (ch + 1 < nch) stream_issue(kr, a.k_st, ch + 1, stage);
+        if (ch + 1 < nch) stream_issue<W>(kr, a.k_st, ch + 1, stage);
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           f32x4 acc[TW][4];
@@ -1081,7 +1092,7 @@ __global__ __launch_bounds__(kStWaves* kWave) void stage1_stream_kernel(Stage1Ar
             }
           }
         }
-        if (ch + 1 < nch) stream_commit(kbuf[(ch + 1) & 1], stage);
+        if (ch + 1 < nch) stream_commit<W>(kbuf[(ch + 1) & 1], stage);
         __syncthreads();
       }
       if (pass == 0) {
@@ -1148,10 +1159,10 @@ int launch_stage1(const Stage1Args& a, hipStream_t s) {
   } else if (a.G == kG && a.D == kD && aligned && a.scale_log2 > 0.f && a.k_st >= kD &&
              (a.out_cols + kStChunkTiles * 16) * a.k_st * 2 < (int64_t{1} << 31) &&
              a.out_cols * static_cast<int64_t>(sizeof(OutT)) < (int64_t{1} << 31)) {
-    constexpr int kTW = 2;
+    constexpr int kTW = kStTokensPerWave;
     const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
     const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
-    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kTW>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW>), dim3(static_cast<unsigned>(grid)),
                        dim3(kStWaves * kWave), 0, s, a, n_rows);
   } else if (a.G == kG && a.D == kD && aligned) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
