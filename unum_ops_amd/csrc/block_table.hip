@@ -4,13 +4,13 @@
 // (src/unum_ops/sparse_kernel_extension/get_table_torch.py:4-44); the exported
 // Triton kernel (get_table_triton.py:6-67) computes the same gather.
 //
-// Work decomposition: one wave owns one (token, head) row of the output --
-// K runs of 64 entries.  The per-token scalars (sequence, position limit,
-// sequence length) are read once per wave; the row's ids are read 64 at a
-// time, one per lane, and broadcast with a lane shuffle; each store step
-// writes four whole runs (1 KiB, one dwordx4 per lane).  The block-table
-// gather for those entries is one dwordx4 load when the four positions are
-// valid, in range and 16-byte aligned, issued eight steps ahead of use.  The
+// Work decomposition: one wave owns 16 ids of one (token, head) row of the
+// output -- 16 runs of 64 entries.  The per-token scalars (sequence, position
+// limit, sequence length) are read once per wave; the ids are read one per
+// lane and broadcast with a lane shuffle; each store step writes four whole
+// runs (1 KiB, one dwordx4 per lane).  The block-table gather for those
+// entries is one dwordx4 load when the four positions are in range and
+// 16-byte aligned, all four steps' loads issued before the first store.  The
 // kernel is bound by the output write.
 #include "common.h"
 
@@ -68,19 +68,31 @@ __device__ __forceinline__ i32x4 finish4(const BlockTableArgs& a, const int32_t*
   return i32x4{v[0], v[1], v[2], v[3]};
 }
 
+// One wave per unit of 16 ids of a (token, head) row: four store steps of
+// four runs.  Units this small give the grid enough waves that the last
+// round of waves is short (whole-row waves left a long tail).
+constexpr int kIdsPerUnit = 16;
+
 template <bool kVecTable>
-__global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a) {
-  const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // t*H + h
-  if (th >= static_cast<int64_t>(a.T) * a.H) return;  // wave-uniform
+__global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a, int64_t n_units,
+                                                          int32_t units_per_row) {
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (unit >= n_units) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
+  const int64_t th = unit / units_per_row;  // t*H + h
+  const int32_t kb = kIdsPerUnit * static_cast<int32_t>(unit - th * units_per_row);
   const int32_t t = static_cast<int32_t>(th / a.H);
   const int32_t h = static_cast<int32_t>(th - static_cast<int64_t>(t) * a.H);
   i32x4* out = reinterpret_cast<i32x4*>(a.out + th * a.K * kSparseBlock);
-  const int32_t sub = lane >> 4;            // run within a store step
-  const int32_t o0 = (lane & 15) * 4;       // first entry of the lane in its run
+  const int32_t sub = lane >> 4;       // run within a store step
+  const int32_t o0 = (lane & 15) * 4;  // first entry of the lane in its run
   const int32_t b = a.token_to_bs[t];
   if (b < 0 || b >= a.B) {
-    for (int32_t q = lane; q < a.K * 16; q += kWave) out[q] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < kIdsPerUnit / 4; ++st) {
+      const int32_t k = kb + 4 * st + sub;
+      if (k < a.K) out[static_cast<int64_t>(k) * 16 + (lane & 15)] = i32x4{0, 0, 0, 0};
+    }
     return;
   }
   const int32_t limit_pos = a.pos[a.pos_scalar ? 0 : t];
@@ -88,42 +100,28 @@ __global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a) {
   const int32_t* row = a.bt + static_cast<int64_t>(b) * a.bt_stride;
   const int32_t* ids = a.topk + static_cast<int64_t>(h) * a.s_h + static_cast<int64_t>(t) * a.s_t;
   const int32_t vec_hi = a.L - 4;  // a dwordx4 at p0 (a multiple of 4) covers p0..p0+3 <= L-1
-  for (int32_t kb = 0; kb < a.K; kb += kWave) {
-    const int32_t my = (kb + lane < a.K) ? ids[static_cast<int64_t>(kb + lane) * a.s_k] : -1;
-    if (kVecTable && a.K - kb >= kWave) {
-      // Sixteen store steps of four runs each, in two batches of eight whose
-      // table loads all go out before the first is used.
+  const int32_t my = (lane < kIdsPerUnit && kb + lane < a.K) ? ids[static_cast<int64_t>(kb + lane) * a.s_k] : -1;
+  // All table loads of the unit go out before the first is used.
+  int32_t p0[kIdsPerUnit / 4];
+  i32x4 raw[kIdsPerUnit / 4];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        int32_t p0[8];
-        i32x4 raw[8];
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-          const int32_t idx = __shfl(my, 4 * (8 * half + st) + sub);
-          p0[st] = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
-          const int32_t safe = (p0[st] >= 0 && p0[st] <= vec_hi) ? p0[st] : 0;
-          raw[st] = *reinterpret_cast<const i32x4*>(row + safe);
-        }
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-          const bool raw_ok = p0[st] >= 0 && p0[st] <= vec_hi;
-          out[static_cast<int64_t>(kb + 4 * (8 * half + st) + sub) * 16 + (lane & 15)] =
-              finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h);
-        }
-      }
+  for (int st = 0; st < kIdsPerUnit / 4; ++st) {
+    const int32_t idx = __shfl(my, 4 * st + sub);
+    p0[st] = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
+    if (kVecTable) {
+      const int32_t safe = (p0[st] >= 0 && p0[st] <= vec_hi) ? p0[st] : 0;
+      raw[st] = *reinterpret_cast<const i32x4*>(row + safe);
     } else {
-      const int32_t steps = (a.K - kb) < kWave ? (a.K - kb + 3) / 4 : kWave / 4;
-      for (int32_t st = 0; st < steps; ++st) {
-        const int32_t k = kb + 4 * st + sub;
-        const int32_t idx = __shfl(my, 4 * st + sub);
-        const int32_t q0 = wrap_add_i32(wrap_mul_i32(idx, kSparseBlock), o0);
-        const bool raw_ok = kVecTable && q0 >= 0 && q0 <= vec_hi;
-        const i32x4 raw = raw_ok ? *reinterpret_cast<const i32x4*>(row + q0) : i32x4{0, 0, 0, 0};
-        if (k < a.K)
-          out[static_cast<int64_t>(k) * 16 + (lane & 15)] =
-              finish4(a, row, raw, raw_ok, q0, limit_len, limit_pos, h);
-      }
+      raw[st] = i32x4{0, 0, 0, 0};
     }
+  }
+#pragma unroll
+  for (int st = 0; st < kIdsPerUnit / 4; ++st) {
+    const int32_t k = kb + 4 * st + sub;
+    const bool raw_ok = kVecTable && p0[st] >= 0 && p0[st] <= vec_hi;
+    if (k < a.K)
+      out[static_cast<int64_t>(k) * 16 + (lane & 15)] =
+          finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h);
   }
 }
 
@@ -185,13 +183,17 @@ extern "C" int unum_get_block_table(const int32_t* topk_idx, int64_t topk_stride
                "get_block_table: output must be 16-byte aligned");
   const bool vec = (reinterpret_cast<uintptr_t>(block_table) & 15) == 0 && (bt_stride_b % 4) == 0 &&
                    L >= 4;
-  const int threads = 256;  // four (token, head) rows per block
-  const int64_t blocks = (T * H + 3) / 4;
+  const int threads = 256;  // four units per block
+  const int32_t units_per_row = (int32_t)((K + kIdsPerUnit - 1) / kIdsPerUnit);
+  const int64_t n_units = T * H * units_per_row;
+  const int64_t blocks = (n_units + 3) / 4;
   UNUM_REQUIRE(blocks <= INT32_MAX, "get_block_table: T*H=%lld too large", (long long)(T * H));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (vec)
-    hipLaunchKernelGGL(block_table_kernel<true>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+    hipLaunchKernelGGL(block_table_kernel<true>, dim3((unsigned)blocks), dim3(threads), 0, s, a,
+                       n_units, units_per_row);
   else
-    hipLaunchKernelGGL(block_table_kernel<false>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+    hipLaunchKernelGGL(block_table_kernel<false>, dim3((unsigned)blocks), dim3(threads), 0, s, a,
+                       n_units, units_per_row);
   return check_launch("get_block_table");
 }
