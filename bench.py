@@ -40,7 +40,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (e.g. under a profiler)")
     ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
-                                       "maxpool_cfg5", "copy"], default=None,
+                                       "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
+                                       "copy"], default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -101,6 +102,7 @@ def main():
 
     from unum_ops_amd import workloads
     from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
+    from unum_ops_amd.pipeline import maxpool_topk
     from unum_ops_amd.sparse_kernel_extension import get_block_table
 
     dev = torch.device("cuda:0")
@@ -135,9 +137,21 @@ def main():
                                      max_context_len=c5["max_context_len"], local_blocks=1,
                                      init_blocks=1)
 
+    def op_topk():
+        return maxpool_topk(mpg["input"], mpg["cu_seqlens_q"], mpg["cu_seqlens_k"],
+                            mpg["cache_lens"], topk=64, **mp_kw)
+
+    def op_topk_cfg5():
+        return maxpool_topk(c5["scores"], c5["cu_q"], c5["cu_k"], c5["cache"],
+                            max_seqlen_q=16 * c5["scores"].shape[-1],
+                            max_context_len=c5["max_context_len"], local_blocks=1,
+                            init_blocks=1, topk=64)
+
     ops = [("stage1", op_stage1), ("maxpool", op_maxpool), ("block_table", op_block_table)]
-    # Timed per kernel only: the long-context configuration's stage 1 and max-pool.
-    extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5)]
+    # Timed per kernel only: the long-context configuration's stage 1 and
+    # max-pool, and the fused pool + top-64 selection on both pool inputs.
+    extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5),
+             ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -219,6 +233,20 @@ def main():
                                      pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
                                      bytes=nbytes,
                                      config="cfg5 scores fp32 [2,4096,8448] -> [2,4096,2112]")
+
+    for name, cu_q, cu_k, nbk in (("maxpool_topk", mp["cu_seqlens_q"], mp["cu_seqlens_k"], 256),
+                                  ("maxpool_topk_cfg5", c5["cu_q_cpu"], c5["cu_k_cpu"],
+                                   -(-c5["max_context_len"] // 64))):
+        if name in per_op:
+            rows = 2 * (int(cu_q[-1]) if name == "maxpool_topk_cfg5" else mp["input"].shape[1])
+            cache = mp["cache_lens"] if name == "maxpool_topk" else [0]
+            nbytes = (workloads.maxpool_bytes(cu_q, cu_k, cache, 2, nbk) - 4 * rows * nbk
+                      + 4 * rows * 64)                   # pooled scores read, ids written
+            t = per_op[name] * 1e-3
+            comps[name] = dict(us=per_op[name] * 1e3, gbs=nbytes / t / 1e9,
+                               pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
+                               config=("cfg2 input" if name == "maxpool_topk" else "cfg5 scores")
+                               + " -> top-64 block ids int32 [2, T, 64]")
 
     cpu = None
     if not args.no_cpu_baseline and "stage1" in comps:

@@ -113,6 +113,30 @@ int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel, int32_t d
                                int32_t local_blocks, int32_t init_blocks, void* stream);
 
 /*
+ * Max-pool fused with the block selection that follows it.  No single
+ * reference function: it is max_pooling_1d_varlen (max_pooling_1d_varlen.py:
+ * 127-183, fp32 input, block_size / stride == 4) followed by the top-k the
+ * reference's tests apply to pooled scores (test/test_sparse_kernel.py:42-43:
+ * top-k ids, sorted ascending), with a deterministic tie-break.
+ *
+ *   topk_idx int32 [H, Tq, topk]: per (h, t), the topk blocks with the largest
+ *            pooled scores, equal scores taken in ascending block id, listed in
+ *            ascending id; a selected block scoring -inf and every slot past
+ *            num_blocks is -1, and the -1 entries come first.
+ *   pooled   optional [H, Tq, num_blocks] fp32 (NULL: not written); when given
+ *            it must be 16-byte aligned with num_blocks % 4 == 0.
+ * Other arguments as unum_max_pooling_1d_varlen.  num_blocks <= 4096; the
+ * input rows must be 16-byte aligned (input aligned, flat_stride % 4 == 0).
+ */
+int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_numel,
+                                    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                    const int32_t* cache_lens, void* pooled, int32_t* topk_idx,
+                                    int64_t H, int64_t Tq, int64_t B, int64_t flat_stride,
+                                    int64_t num_blocks, int32_t block_size, int32_t stride,
+                                    int32_t local_blocks, int32_t init_blocks, int32_t topk,
+                                    void* stream);
+
+/*
  * Top-k block ids -> per-token paged KV slots, replacing
  * get_block_table_ref_torch (get_table_torch.py:4-44) and the exported
  * get_block_table_v2/_v3 (get_table_triton.py:218-264, kernel :6-67).

@@ -11,6 +11,9 @@ path (Yanguan619/unum_ops):
 * ``infllmv2_attn_stage1``   -- fp32 torch-CPU restatement of the Triton v2
   kernel ``src/unum_ops/infllm_v2/infllmv2_attn_stage1_triton_v2.py:20-228``
   (the exported ``infllmv2_attn_stage1``).
+* ``topk_blocks``            -- the block selection over pooled scores
+  (top-k, ids sorted ascending as in ``test/test_sparse_kernel.py:42-43``),
+  with the build's tie-break (equal scores by ascending id).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker / the timed CPU
@@ -31,6 +34,8 @@ fails a check that does not retype the same formula):
   uniform-softmax closed form ``G / vis`` that pins the causal visible count,
   a hand-derived table of visible counts (truncating division), and row-sum
   invariants.
+* top-k: a Python ``sorted`` brute force over (score, id) pairs, and
+  ``torch.topk`` (a library routine) on rows with distinct scores.
 
 All three functions are pinned; none is "parity unpinned".
 """
@@ -38,6 +43,7 @@ All three functions are pinned; none is "parity unpinned".
 from .block_table import get_block_table
 from .maxpool import max_pooling_1d_varlen
 from .stage1 import infllmv2_attn_stage1, visible_counts, tdiv
+from .topk import topk_blocks
 
 __all__ = [
     "get_block_table",
@@ -45,4 +51,5 @@ __all__ = [
     "infllmv2_attn_stage1",
     "visible_counts",
     "tdiv",
+    "topk_blocks",
 ]

@@ -1,0 +1,84 @@
+"""GPU parity of the fused max-pool + block top-k kernel (bit-exact).
+
+The block ids must equal the oracle's selection (equal scores by ascending
+id, ``-1`` for ``-inf`` blocks and missing slots, ``-1`` first) on the oracle's
+pooled scores of the same input, and the optional pooled output must equal
+the oracle's max-pool bit for bit.  Inputs the fused kernel does not take run
+the unfused pair and must give the same result.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.maxpool import max_pooling_1d_varlen as oracle_pool
+from oracle.topk import topk_blocks as oracle_topk
+from unum_ops_amd import workloads
+from unum_ops_amd.pipeline import maxpool_topk
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(d, dev, topk, return_pooled=True, **kw):
+    res = maxpool_topk(d["input"].to(dev), d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev),
+                       d["cache_lens"].to(dev), topk=topk, return_pooled=return_pooled, **kw)
+    torch.cuda.synchronize()
+    idx, pooled = res if return_pooled else (res, None)
+    exp_pool = oracle_pool(d["input"], d["cu_seqlens_q"], d["cu_seqlens_k"], d["cache_lens"],
+                           oob="absent", **kw)
+    if pooled is not None:
+        np.testing.assert_array_equal(pooled.float().cpu().numpy(), exp_pool)
+    exp_idx = oracle_topk(exp_pool, topk)
+    assert idx.dtype == torch.int32 and tuple(idx.shape) == exp_idx.shape
+    np.testing.assert_array_equal(idx.cpu().numpy(), exp_idx)
+    return idx
+
+
+def _kw(max_seqlen_q, max_context_len, local_blocks=1, init_blocks=1):
+    return dict(max_seqlen_q=max_seqlen_q, max_context_len=max_context_len,
+                local_blocks=local_blocks, init_blocks=init_blocks)
+
+
+@pytest.mark.parametrize("local_blocks", [1, 2])
+def test_cfg2(local_blocks, dev):
+    d = workloads.cfg2_maxpool(local_blocks=local_blocks)
+    _check(d, dev, 64, **_kw(16384, 16384, local_blocks))
+
+
+def test_long_rows_2112_blocks(dev):
+    # cfg5's pooled width: 8447 compressed keys per row, flat stride 8448
+    d = workloads.maxpool_inputs([300, 211], F=8448, H=2, seed=5, k_lens=[8447, 5000])
+    _check(d, dev, 64, **_kw(16 * 8448, 135168))
+
+
+@pytest.mark.parametrize("topk", [1, 7, 64, 100])
+def test_ties_everywhere(topk, dev):
+    # few distinct scores: the tie-break decides most of the selection
+    d = workloads.maxpool_inputs([70, 33, 129], F=1024, H=2, seed=6)
+    x = d["input"]
+    d["input"] = torch.where(x > 0, torch.floor(x * 4096.0) / 8.0, x)
+    _check(d, dev, topk, **_kw(16384, 64 * 200, 2, 3))
+
+
+def test_fewer_blocks_than_topk(dev):
+    d = workloads.maxpool_inputs([40, 9], F=128, H=2, seed=7, k_lens=[50, 20])
+    _check(d, dev, 64, **_kw(2048, 1000))           # 16 blocks < 64
+
+
+def test_block_count_not_multiple_of_four(dev):
+    d = workloads.maxpool_inputs([40, 90], F=256, H=2, seed=8)
+    _check(d, dev, 8, return_pooled=False, **_kw(4096, 64 * 13))   # 13 blocks, fused
+    _check(d, dev, 8, return_pooled=True, **_kw(4096, 64 * 13))    # pooled asked: unfused
+
+
+def test_tokens_outside_sequences(dev):
+    d = workloads.maxpool_inputs([50, 30], F=512, H=2, seed=9)
+    d["cu_seqlens_q"] = torch.tensor([0, 20, 60], dtype=torch.int32)  # tokens 60..79 orphan
+    _check(d, dev, 16, **_kw(8192, 8192))
+
+
+def test_unfused_shapes(dev):
+    d = workloads.maxpool_inputs([64, 20], F=1100, H=2, seed=10, k_lens=[1050, 400])
+    _check(d, dev, 32, **_kw(16 * 1100, 64 * 4100))     # 4100 blocks > 4096
+    db = dict(d, input=d["input"].to(torch.bfloat16))
+    _check(db, dev, 32, **_kw(16 * 1100, 64 * 300))     # bf16 input

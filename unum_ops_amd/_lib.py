@@ -54,6 +54,16 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32,    # block_size, stride, local_blocks, init_blocks
         _p,                        # stream
     ]),
+    "unum_max_pooling_1d_varlen_topk": (ctypes.c_int, [
+        _p, _i64,                  # input, input_numel
+        _p, _p, _p,                # cu_seqlens_q, cu_seqlens_k, cache_lens
+        _p, _p,                    # pooled (may be NULL), topk_idx
+        _i64, _i64, _i64,          # H, Tq, B
+        _i64, _i64,                # flat_stride, num_blocks
+        _i32, _i32, _i32, _i32,    # block_size, stride, local_blocks, init_blocks
+        _i32,                      # topk
+        _p,                        # stream
+    ]),
     "unum_get_block_table": (ctypes.c_int, [
         _p, _i64, _i64, _i64,      # topk_idx + strides (h, t, k)
         _p, _i64,                  # block_table, row stride

@@ -139,43 +139,46 @@ __device__ __forceinline__ void store4(void* out, int64_t o, const float* r) {
   }
 }
 
-template <typename T, bool kVec>
-__global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
-  const int64_t u = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (u >= a.n_units) return;  // wave-uniform
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = u / a.n_chunks;  // h*Tq + t
-  const int64_t chunk = u - row * a.n_chunks;
-  const int64_t t = row % a.Tq;
+// Row context of the P == 4 path: key length, block of the token, flat row
+// start and the tap limit.
+struct RowCtx {
+  int64_t lk, ob, base, lim;
+};
 
+__device__ __forceinline__ RowCtx row_ctx(const PoolArgs& a, int64_t row) {
+  const int64_t t = row % a.Tq;
   const int b = find_sequence(a.cu_q, a.B, t);
-  int64_t lk = 0, ob = 0;
+  RowCtx c{0, 0, row * a.F, 0};
   if (b >= 0) {
-    lk = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
-    ob = (t - a.cu_q[b]) / a.block_size;
+    c.lk = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
+    c.ob = (t - a.cu_q[b]) / a.block_size;
   }
-  const int64_t base = row * a.F;
   // Taps are present below the key length, inside the input, and below the
   // last tap any output window uses (4*NB - 1).
-  int64_t lim = lk < (a.numel - base) ? lk : (a.numel - base);
-  lim = lim < 4 * a.NB ? lim : 4 * a.NB;
+  int64_t lim = c.lk < (a.numel - c.base) ? c.lk : (a.numel - c.base);
+  c.lim = lim < 4 * a.NB ? lim : 4 * a.NB;
+  return c;
+}
 
+// Pooled outputs n0..n0+3 (n0 = 256*chunk + 4*lane) of a row.
+template <typename T, bool kVec>
+__device__ __forceinline__ void pool4(const PoolArgs& a, const RowCtx& c, int64_t chunk, float* r) {
+  const int lane = threadIdx.x & (kWave - 1);
   const int64_t n0 = chunk * 256 + 4 * lane;
   const int64_t p0 = 4 * n0;
   float v[16];
-  if (kVec && p0 + 15 < lim) {
-    Vec16<T>::load(a.in, base + p0, v);
+  if (kVec && p0 + 15 < c.lim) {
+    Vec16<T>::load(a.in, c.base + p0, v);
   } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
-      v[j] = (p0 + j < lim) ? Elem<T>::load(a.in, base + p0 + j) : -INFINITY;
+      v[j] = (p0 + j < c.lim) ? Elem<T>::load(a.in, c.base + p0 + j) : -INFINITY;
   }
   float prev = __shfl_up(v[15], 1);
   if (lane == 0) {
     const int64_t pe = p0 - 1;
-    prev = (pe >= 0 && pe < lim) ? Elem<T>::load(a.in, base + pe) : -INFINITY;
+    prev = (pe >= 0 && pe < c.lim) ? Elem<T>::load(a.in, c.base + pe) : -INFINITY;
   }
-  float r[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t n = n0 + e;
@@ -184,18 +187,148 @@ __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
                           fmaxf(fmaxf(v[4 * e + 1], v[4 * e + 2]), v[4 * e + 3]));
     const int64_t ws = 4 * n - 1;
     const int64_t w_lo = ws < 0 ? 0 : ws;
-    const int64_t w_hi = (ws + 5) < lk ? (ws + 5) : lk;
-    const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
+    const int64_t w_hi = (ws + 5) < c.lk ? (ws + 5) : c.lk;
+    const bool force = n < a.init_blocks || (c.ob >= n && c.ob <= n + a.local_blocks);
     r[e] = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
   }
-  const int64_t o = row * a.NB + n0;
+}
+
+template <typename T, bool kVec>
+__device__ __forceinline__ void store_pooled(const PoolArgs& a, int64_t row, int64_t n0, const float* r) {
   if (n0 >= a.NB) return;
+  const int64_t o = row * a.NB + n0;
   if (kVec && n0 + 3 < a.NB) {
     store4<T>(a.out, o, r);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       if (n0 + e < a.NB) Elem<T>::store(a.out, o + e, r[e]);
+  }
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
+  const int64_t u = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  if (u >= a.n_units) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = u / a.n_chunks;  // h*Tq + t
+  const int64_t chunk = u - row * a.n_chunks;
+  const RowCtx c = row_ctx(a, row);
+  float r[4];
+  pool4<T, kVec>(a, c, chunk, r);
+  store_pooled<T, kVec>(a, row, chunk * 256 + 4 * lane, r);
+}
+
+// ------------------------------------------------------- fused block top-k
+// The selection the pipeline makes from the pooled scores, fused into the
+// pool: one wave per (head, token) row pools all NB blocks into registers
+// (the P == 4 path above; optionally storing them) and writes the row's top K
+// block ids under the order (score descending, block id ascending), sorted
+// ascending, with -1 for a selected block whose score is -inf and for the
+// slots past NB -- the -1 entries first.
+//
+// Selection: scores map to order-preserving unsigned keys; a threshold is
+// built bit by bit from the top (each step a ballot count of the keys at or
+// above a candidate) until it is the K-th largest key or exactly K keys lie
+// at or above it; keys above it are taken, and of the keys equal to it the
+// ones with the lowest block ids, by a running rank.
+constexpr int kTopkMaxChunks = 16;  // NB <= 4096 (64 keys per lane)
+constexpr uint32_t kKeyNegInf = 0x007fffffu;  // order_key(-inf)
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Lanes below this one whose bit is set in mask.
+__device__ __forceinline__ int32_t lanes_below(uint64_t mask) {
+  return static_cast<int32_t>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* topk, int32_t K,
+                                                           int32_t store) {
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  if (row >= a.H * a.Tq) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const RowCtx c = row_ctx(a, row);
+  const int32_t NB = static_cast<int32_t>(a.NB);
+  // Keys of blocks n = 256*ch + 4*lane + e; 0 (below every real key) past NB.
+  uint32_t key[NCH][4];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    float r[4];
+    pool4<float, true>(a, c, ch, r);
+    if (store) store_pooled<float, true>(a, row, ch * 256 + 4 * lane, r);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[ch][e] = (256 * ch + 4 * lane + e < NB) ? order_key(r[e]) : 0u;
+  }
+  auto count_ge = [&](uint32_t cand) -> int32_t {
+    int32_t n = 0;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) n += __popcll(__ballot(key[ch][e] >= cand));
+    return n;
+  };
+  uint32_t tau = 0;     // the K-th largest key (0 when every block is taken)
+  int32_t need_eq = 0;  // blocks with key == tau to take, lowest ids first
+  int32_t neg = 0;      // taken blocks scoring -inf
+  if (NB > K) {
+    // A candidate with exactly K keys at or above it decides the selection
+    // (keys >= it); the lower bits are then not needed, and the tie rule
+    // below takes every key equal to it.
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = tau | (1u << bit);
+      const int32_t n = count_ge(cand);
+      if (n >= K) tau = cand;
+      if (n == K) break;
+    }
+    need_eq = K - (tau == 0xffffffffu ? 0 : count_ge(tau + 1));
+    neg = tau == kKeyNegInf ? need_eq : 0;
+  } else {
+    neg = count_ge(kKeyNegInf) - count_ge(kKeyNegInf + 1);
+  }
+  int32_t* orow = topk + row * K;
+  int32_t lead = (NB < K ? K - NB : 0) + neg;  // -1 slots, first
+  lead = lead < K ? lead : K;
+  for (int32_t j = lane; j < lead; j += kWave) orow[j] = -1;
+  int32_t out_pos = lead, eq_seen = 0;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    bool eq[4];
+    uint64_t m_eq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      eq[e] = key[ch][e] == tau && need_eq > 0;
+      m_eq[e] = __ballot(eq[e]);
+    }
+    int32_t eq_rank = eq_seen;  // equal keys at lower block ids
+#pragma unroll
+    for (int e = 0; e < 4; ++e) eq_rank += lanes_below(m_eq[e]);
+    bool take[4];
+    uint64_t m_take[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool sel = key[ch][e] > tau || (eq[e] && eq_rank < need_eq);
+      eq_rank += eq[e] ? 1 : 0;
+      take[e] = sel && key[ch][e] != kKeyNegInf;
+      m_take[e] = __ballot(take[e]);
+    }
+    int32_t pos = out_pos;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pos += lanes_below(m_take[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (take[e] && pos < K) orow[pos] = 256 * ch + 4 * lane + e;
+      pos += take[e] ? 1 : 0;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      out_pos += __popcll(m_take[e]);
+      eq_seen += __popcll(m_eq[e]);
+    }
   }
 }
 
@@ -255,6 +388,25 @@ int launch_pool(const PoolArgs& a, hipStream_t s) {
   return check_launch("max_pooling_1d_varlen");
 }
 
+int launch_topk(const PoolArgs& a, int32_t* topk, int32_t K, int32_t store, hipStream_t s) {
+  const int nch = static_cast<int>((a.NB + 255) / 256);
+  const int64_t blocks = (a.H * a.Tq * kWave + 255) / 256;
+  if (blocks > INT32_MAX) UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen_topk: too many rows");
+  const dim3 g(static_cast<unsigned>(blocks)), b(256);
+  switch (nch) {
+#define UNUM_TOPK_CASE(N) \
+    case N: hipLaunchKernelGGL((maxpool_topk_kernel<N>), g, b, 0, s, a, topk, K, store); break;
+    UNUM_TOPK_CASE(1) UNUM_TOPK_CASE(2) UNUM_TOPK_CASE(3) UNUM_TOPK_CASE(4)
+    UNUM_TOPK_CASE(5) UNUM_TOPK_CASE(6) UNUM_TOPK_CASE(7) UNUM_TOPK_CASE(8)
+    UNUM_TOPK_CASE(9) UNUM_TOPK_CASE(10) UNUM_TOPK_CASE(11) UNUM_TOPK_CASE(12)
+    UNUM_TOPK_CASE(13) UNUM_TOPK_CASE(14) UNUM_TOPK_CASE(15) UNUM_TOPK_CASE(16)
+#undef UNUM_TOPK_CASE
+    default: UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "max_pooling_1d_varlen_topk: %lld blocks (max %d)",
+                       (long long)a.NB, kTopkMaxChunks * 256);
+  }
+  return check_launch("max_pooling_1d_varlen_topk");
+}
+
 }  // namespace
 }  // namespace unum
 
@@ -308,4 +460,60 @@ extern "C" int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel
     case UNUM_DTYPE_F16: return launch_pool<_Float16>(a, s);
     default: UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "max_pooling_1d_varlen: unsupported dtype %d", dtype);
   }
+}
+
+extern "C" int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_numel,
+                                               const int32_t* cu_seqlens_q,
+                                               const int32_t* cu_seqlens_k,
+                                               const int32_t* cache_lens, void* pooled,
+                                               int32_t* topk_idx, int64_t H, int64_t Tq,
+                                               int64_t B, int64_t flat_stride,
+                                               int64_t num_blocks, int32_t block_size,
+                                               int32_t stride, int32_t local_blocks,
+                                               int32_t init_blocks, int32_t topk, void* stream) {
+  using namespace unum;
+  clear_error();
+  UNUM_REQUIRE(H >= 0 && Tq >= 0 && B >= 0 && num_blocks >= 0 && flat_stride >= 0,
+               "max_pooling_1d_varlen_topk: negative size");
+  UNUM_REQUIRE(topk >= 1, "max_pooling_1d_varlen_topk: topk=%d", topk);
+  UNUM_REQUIRE(block_size > 0 && stride > 0 && block_size / stride == 4,
+               "max_pooling_1d_varlen_topk: block_size / stride must be 4 (got %d / %d)",
+               block_size, stride);
+  UNUM_REQUIRE(num_blocks <= kTopkMaxChunks * 256,
+               "max_pooling_1d_varlen_topk: %lld blocks exceed %d", (long long)num_blocks,
+               kTopkMaxChunks * 256);
+  if (H == 0 || Tq == 0) return UNUM_OK;
+  UNUM_REQUIRE(num_blocks >= 1, "max_pooling_1d_varlen_topk: no blocks");
+  UNUM_REQUIRE(input && topk_idx && cu_seqlens_q && cu_seqlens_k && cache_lens,
+               "max_pooling_1d_varlen_topk: null pointer");
+  UNUM_REQUIRE(B >= 1, "max_pooling_1d_varlen_topk: cu_seqlens must hold at least 2 entries");
+  UNUM_REQUIRE(H * Tq * flat_stride <= input_numel,
+               "max_pooling_1d_varlen_topk: flat row stride %lld times H*Tq=%lld rows exceeds "
+               "the input's %lld elements",
+               (long long)flat_stride, (long long)(H * Tq), (long long)input_numel);
+  UNUM_REQUIRE((reinterpret_cast<uintptr_t>(input) & 15) == 0 && (flat_stride % 4) == 0,
+               "max_pooling_1d_varlen_topk: input rows must be 16-byte aligned");
+  UNUM_REQUIRE(pooled == nullptr ||
+                   ((reinterpret_cast<uintptr_t>(pooled) & 15) == 0 && (num_blocks % 4) == 0),
+               "max_pooling_1d_varlen_topk: the pooled output needs 16-byte aligned rows "
+               "(num_blocks %% 4 == 0)");
+  PoolArgs a;
+  a.in = input;
+  a.numel = input_numel;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.cache = cache_lens;
+  a.out = pooled;
+  a.H = H;
+  a.Tq = Tq;
+  a.B = B;
+  a.F = flat_stride;
+  a.NB = num_blocks;
+  a.block_size = block_size;
+  a.P = 4;
+  a.local_blocks = local_blocks;
+  a.init_blocks = init_blocks;
+  a.n_chunks = (num_blocks + 255) / 256;
+  a.n_units = H * Tq * a.n_chunks;
+  return launch_topk(a, topk_idx, topk, pooled != nullptr ? 1 : 0, static_cast<hipStream_t>(stream));
 }

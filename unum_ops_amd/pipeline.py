@@ -10,7 +10,8 @@ follows from the layouts of its three ops:
    ``max_seqlen_q // 16``, so the pipeline passes ``max_seqlen_q = 16 * Kp``
    and each row is read in place (``max_pooling_1d_varlen.py:127-183``);
 3. a top-k picks the ``topk`` best 64-token blocks per (head, token), ties
-   going to the lower block id;
+   going to the lower block id (fused with step 2 in one kernel,
+   ``maxpool_topk``);
    the ids are sorted ascending as the reference's tests sort them
    (``test/test_sparse_kernel.py:42-43``) and blocks whose pooled score is
    ``-inf`` (no compressed key in the window) become ``-1``;
@@ -26,9 +27,12 @@ import math
 
 import torch
 
-from ._common import require_gpu
+from . import _lib
+from ._common import as_i32, as_int, require_gpu
 from .infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
 from .sparse_kernel_extension import get_block_table
+
+FUSED_MAX_BLOCKS = 4096  # the fused pool + top-k kernel keeps a row's blocks in registers
 
 
 def topk_blocks(pooled, topk):
@@ -48,6 +52,62 @@ def topk_blocks(pooled, topk):
         pad = torch.full((H, T, topk - k), -1, dtype=torch.int32, device=pooled.device)
         idx = torch.cat([pad, idx], dim=-1)
     return idx
+
+
+def maxpool_topk(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seqlen_q, max_context_len,
+                 local_blocks, init_blocks, block_size=64, stride=16, topk=64,
+                 return_pooled=False):
+    """``topk_blocks(max_pooling_1d_varlen(...), topk)`` in one kernel.
+
+    The arguments are those of ``max_pooling_1d_varlen`` plus ``topk``.
+    Returns the int32 block ids ``[H, Tq, topk]`` (or ``(ids, pooled)`` with
+    ``return_pooled``).  One gfx950 kernel pools each row into registers and
+    selects its blocks, so the pooled scores never go through HBM unless
+    asked for.  Inputs the fused kernel does not take (a dtype other than fp32,
+    ``block_size / stride != 4``, more than 4096 blocks, unaligned rows) run the
+    two ops separately, with the same result.
+    """
+    op = "maxpool_topk"
+    dev = require_gpu(op, input, cu_seqlens_q, cu_seqlens_k, cache_lens)
+    if input.dim() != 3:
+        raise ValueError(f"{op}: input must be [H, total_q, *]")
+    topk = as_int(topk, "topk", op)
+    if topk < 1:
+        raise ValueError(f"{op}: topk must be >= 1, got {topk}")
+    H, n_q, _ = input.shape
+    max_seqlen_q = as_int(max_seqlen_q, "max_seqlen_q", op)
+    max_context_len = as_int(max_context_len, "max_context_len", op)
+    nb = math.ceil(max_context_len / block_size)
+    flat_stride = max_seqlen_q // stride
+    x = input if input.is_contiguous() else input.contiguous()
+    fused = (x.dtype == torch.float32 and block_size // stride == 4 and block_size > 0
+             and 1 <= nb <= FUSED_MAX_BLOCKS and flat_stride % 4 == 0
+             and x.data_ptr() % 16 == 0 and (not return_pooled or nb % 4 == 0))
+    if not fused:
+        pooled = max_pooling_1d_varlen(x, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seqlen_q,
+                                       max_context_len, local_blocks, init_blocks,
+                                       block_size=block_size, stride=stride)
+        idx = topk_blocks(pooled, topk)
+        return (idx, pooled) if return_pooled else idx
+    idx = torch.empty(H, n_q, topk, dtype=torch.int32, device=dev)
+    pooled = torch.empty(H, n_q, nb, dtype=x.dtype, device=dev) if return_pooled else None
+    if idx.numel() == 0:
+        return (idx, pooled) if return_pooled else idx
+    batch = cu_seqlens_q.shape[0] - 1
+    cu_q = as_i32(cu_seqlens_q, "cu_seqlens_q", op)
+    cu_k = as_i32(cu_seqlens_k, "cu_seqlens_k", op)
+    cache = as_i32(cache_lens, "cache_lens", op).reshape(-1)
+    if cu_k.numel() < batch + 1 or cache.numel() < batch:
+        raise ValueError(f"{op}: cu_seqlens_k / cache_lens shorter than the batch ({batch})")
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.unum_max_pooling_1d_varlen_topk(
+            _lib.ptr(x), x.numel(), _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(cache),
+            _lib.ptr(pooled), _lib.ptr(idx), H, n_q, batch, flat_stride, nb,
+            int(block_size), int(stride), int(local_blocks), int(init_blocks), topk,
+            _lib.stream_ptr(dev))
+    _lib.check(st, op)
+    return (idx, pooled) if return_pooled else idx
 
 
 def select_blocks(q, k, cu_seqlens_q, cu_seqlens_k, block_table, token_to_bs, token_pos_in_bs,
@@ -73,11 +133,11 @@ def select_blocks(q, k, cu_seqlens_q, cu_seqlens_k, block_table, token_to_bs, to
     kp = scores.shape[-1]
     batch = cu_seqlens_q.numel() - 1
     cache = torch.zeros(max(batch, 1), dtype=torch.int32, device=dev)
-    pooled = max_pooling_1d_varlen(scores, cu_seqlens_q, cu_seqlens_k, cache,
-                                   max_seqlen_q=stride * kp, max_context_len=max_context_len,
-                                   local_blocks=local_blocks, init_blocks=init_blocks,
-                                   block_size=block_size, stride=stride)
-    idx = topk_blocks(pooled, topk)
+    res = maxpool_topk(scores, cu_seqlens_q, cu_seqlens_k, cache, max_seqlen_q=stride * kp,
+                       max_context_len=max_context_len, local_blocks=local_blocks,
+                       init_blocks=init_blocks, block_size=block_size, stride=stride,
+                       topk=topk, return_pooled=return_intermediates)
+    idx, pooled = res if return_intermediates else (res, None)
     table = get_block_table(idx, block_table, token_to_bs, token_pos_in_bs, seqlen_q,
                             head_group=head_group)
     if return_intermediates:
@@ -90,4 +150,4 @@ def num_blocks(max_context_len, block_size=64):
     return math.ceil(max_context_len / block_size)
 
 
-__all__ = ["select_blocks", "topk_blocks", "num_blocks"]
+__all__ = ["select_blocks", "maxpool_topk", "topk_blocks", "num_blocks"]
