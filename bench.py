@@ -41,7 +41,7 @@ def parse():
                     help="skip the CPU oracle timing (e.g. under a profiler)")
     ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
                                        "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
-                                       "copy"], default=None,
+                                       "compress_keys_cfg5", "copy"], default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -79,8 +79,10 @@ def build_inputs(dev):
               token_to_bs=p5["token_to_bs"].to(dev), token_pos_in_bs=p5["token_pos_in_bs"].to(dev),
               seqlen_q=p5["seqlen_q"].to(dev))
     # cfg5's stage 1 and max-pool are timed too (reported as components, not
-    # part of the headline step).
-    c5 = dict(q=q5, k=k5, cu_q=cu_q5, cu_k=cu_k5, max_seqlen_k=p5["max_seqlen_k"],
+    # part of the headline step), and key compression on its raw keys.
+    raw5 = torch.randn(135168, 2, 128, generator=torch.Generator().manual_seed(5)).to(
+        torch.bfloat16).to(dev)
+    c5 = dict(raw=raw5, cu_raw=torch.tensor([0, 135168], dtype=torch.int32, device=dev),q=q5, k=k5, cu_q=cu_q5, cu_k=cu_k5, max_seqlen_k=p5["max_seqlen_k"],
               max_context_len=p5["max_context_len"], scores=sc,
               cache=torch.zeros(1, dtype=torch.int32, device=dev),
               cu_q_cpu=p5["cu_seqlens_q"], cu_k_cpu=p5["cu_seqlens_k"])
@@ -102,6 +104,7 @@ def main():
 
     from unum_ops_amd import workloads
     from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
+    from unum_ops_amd.compression import CompressionPlan, compress_keys
     from unum_ops_amd.pipeline import maxpool_topk
     from unum_ops_amd.sparse_kernel_extension import get_block_table
 
@@ -147,11 +150,18 @@ def main():
                             max_context_len=c5["max_context_len"], local_blocks=1,
                             init_blocks=1, topk=64)
 
+    plan5 = CompressionPlan(torch.tensor([0, 135168]), 2, 128, dev)
+
+    def op_compress_cfg5():
+        return compress_keys(c5["raw"], c5["cu_raw"], plan=plan5)
+
     ops = [("stage1", op_stage1), ("maxpool", op_maxpool), ("block_table", op_block_table)]
     # Timed per kernel only: the long-context configuration's stage 1 and
-    # max-pool, and the fused pool + top-64 selection on both pool inputs.
+    # max-pool, the fused pool + top-64 selection on both pool inputs, and key
+    # compression of cfg5's raw keys.
     extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5),
-             ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5)]
+             ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5),
+             ("compress_keys_cfg5", op_compress_cfg5)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -247,6 +257,17 @@ def main():
                                pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
                                config=("cfg2 input" if name == "maxpool_topk" else "cfg5 scores")
                                + " -> top-64 block ids int32 [2, T, 64]")
+
+    if "compress_keys_cfg5" in per_op:
+        nbytes = 2 * 135168 * 2 * 128 + 2 * 8447 * 2 * 128
+        t = per_op["compress_keys_cfg5"] * 1e-3
+        comps["compress_keys_cfg5"] = dict(us=per_op["compress_keys_cfg5"] * 1e3,
+                                           gbs=nbytes / t / 1e9,
+                                           pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                           bytes=nbytes,
+                                           config="cfg5 raw keys bf16 [135168,2,128] -> "
+                                                  "[8447,2,128] (kernel 32, stride 16), "
+                                                  "planned (no host sync)")
 
     cpu = None
     if not args.no_cpu_baseline and "stage1" in comps:

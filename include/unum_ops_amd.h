@@ -165,6 +165,30 @@ int unum_get_block_table(const int32_t* topk_idx, int64_t topk_stride_h,
                          int32_t* out, int64_t H, int64_t T, int64_t K, int64_t B,
                          int64_t L, int32_t head_group, void* stream);
 
+/*
+ * Key compression: mean-pool raw keys into the compressed keys stage 1 takes.
+ * No reference function: the reference's stage 1 receives compressed keys;
+ * the pooling (kernel 32, stride 16) is the one its benchmark configurations
+ * describe ("compressed k ... built as mean-pooled blocks of raw keys").
+ *
+ *   k      bf16 [T_raw, H, D], element strides (k_stride_t, k_stride_h, 1)
+ *   cu_seqlens_raw  int32 [B+1]; cu_seqlens_comp int32 [B+1] with
+ *          Lk_b = (L_b - kernel_size) / stride + 1 (0 if L_b < kernel_size)
+ *   unit_prefix int32 [B+1]: first work unit of each sequence,
+ *          units_b = ceil(Lk_b / windows_per_unit); n_units = unit_prefix[B]
+ *   out    bf16 [T_comp, H, D] contiguous:
+ *          out[cu_comp[b]+j] = bf16_rne(((h_j + h_{j+1}) / kernel_size)),
+ *          h_m = sum over the stride tokens stride*m .. stride*m+stride-1 of
+ *          the sequence, in fp32 in token order.
+ * kernel_size == 2 * stride == 32; D % 8 == 0 and H*D/8 <= 64;
+ * windows_per_unit a multiple of 64 / (H*D/8).
+ */
+int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                       const int32_t* cu_seqlens_raw, const int32_t* cu_seqlens_comp,
+                       const int32_t* unit_prefix, int64_t n_units, void* out, int64_t B,
+                       int64_t T_raw, int64_t T_comp, int64_t H, int64_t D, int32_t kernel_size,
+                       int32_t stride, int32_t windows_per_unit, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

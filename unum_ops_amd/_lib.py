@@ -64,6 +64,14 @@ SIGNATURES = {
         _i32,                      # topk
         _p,                        # stream
     ]),
+    "unum_compress_keys": (ctypes.c_int, [
+        _p, _i64, _i64,            # k, k_stride_t, k_stride_h
+        _p, _p, _p, _i64,          # cu_seqlens_raw, cu_seqlens_comp, unit_prefix, n_units
+        _p,                        # out
+        _i64, _i64, _i64, _i64, _i64,  # B, T_raw, T_comp, H, D
+        _i32, _i32, _i32,          # kernel_size, stride, windows_per_unit
+        _p,                        # stream
+    ]),
     "unum_get_block_table": (ctypes.c_int, [
         _p, _i64, _i64, _i64,      # topk_idx + strides (h, t, k)
         _p, _i64,                  # block_table, row stride

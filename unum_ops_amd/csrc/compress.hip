@@ -1,0 +1,171 @@
+// compress_keys: mean-pool raw keys into the compressed keys stage 1 scores
+// against (kernel 32, stride 16 in the benchmark configurations).
+//
+// The reference has no kernel for this step (its stage 1 takes compressed
+// keys as input); the definition is the mean of each window of `kernel`
+// consecutive tokens of a sequence, windows `stride` apart:
+//   Lk_b = (L_b - kernel) / stride + 1   (0 if L_b < kernel)
+//   kc[j] = (1/kernel) * sum_{i < kernel} k[16j + i]     (per head, per dim)
+// With kernel == 2*stride each window is two half-blocks:
+//   h_j   = sum_{i < stride} k[stride*j + i]   (fp32, in token order)
+//   kc[j] = bf16_rne((h_j + h_{j+1}) * (1/kernel))
+// The summation order is fixed, so the result is reproducible bit for bit
+// (kernel a power of two: the scale is exact).
+//
+// Work decomposition: a wave owns a unit of consecutive windows of one
+// sequence; each lane owns one 8-element slice (16 bytes) of one head, a row
+// of the group's lanes covering all heads and dims of a token, and the
+// wave's lane groups split the unit's windows between them.  A lane issues
+// all 32 token loads of a window at once (each raw key is read from HBM
+// once; the half-block two windows share comes the second time from L2).
+#include "common.h"
+
+namespace unum {
+namespace {
+
+struct CompressArgs {
+  const __bf16* k;
+  int64_t k_st, k_sh;
+  const int32_t* cu_raw;
+  const int32_t* cu_comp;
+  const int32_t* unit_prefix;  // [B+1]: first unit of each sequence
+  uint16_t* out;               // [T_comp, H, D] bf16 bits
+  int64_t B, n_units, T_raw, T_comp;
+  int32_t H, D, stride, per_group;  // windows per lane group
+  float inv_kernel;
+};
+
+__device__ __forceinline__ int find_seq(const int32_t* prefix, int64_t B, int64_t u) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int count = 0;
+  for (int64_t base = 0; base <= B; base += kWave) {
+    const int64_t i = base + lane;
+    const bool le = (i <= B) && (prefix[i] <= u);
+    count += __popcll(__ballot(le));
+  }
+  return count - 1;
+}
+
+__device__ __forceinline__ void add8(float* acc, i32x4 w) {
+  const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    acc[2 * e] += __uint_as_float(u[e] << 16);
+    acc[2 * e + 1] += __uint_as_float(u[e] & 0xffff0000u);
+  }
+}
+
+// Window j of a lane's slice: the 2*kStride token rows 16j .. are loaded
+// together, then each half-block is summed in token order.
+template <int kStride>
+__device__ __forceinline__ void window(const __bf16* kb, int64_t k_st, int64_t j, float* h0,
+                                       float* h1) {
+  i32x4 w[2 * kStride];
+#pragma unroll
+  for (int i = 0; i < 2 * kStride; ++i)
+    w[i] = *reinterpret_cast<const i32x4*>(kb + (j * kStride + i) * k_st);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h0[e] = h1[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kStride; ++i) add8(h0, w[i]);
+#pragma unroll
+  for (int i = 0; i < kStride; ++i) add8(h1, w[kStride + i]);
+}
+
+template <int kStride>
+__global__ __launch_bounds__(256) void compress_keys_kernel(CompressArgs a) {
+  const int64_t unit = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  if (unit >= a.n_units) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const int b = find_seq(a.unit_prefix, a.B, unit);
+  if (b < 0 || b >= a.B) return;
+  const int32_t slices = a.D / 8;               // 16-byte slices per head
+  const int32_t row_lanes = a.H * slices;       // lanes per token row
+  const int32_t groups = kWave / row_lanes;
+  const int32_t grp = lane / row_lanes;
+  if (grp >= groups) return;                    // lanes past the last full group
+  const int32_t h = (lane % row_lanes) / slices;
+  const int32_t d0 = 8 * ((lane % row_lanes) % slices);
+  const int64_t run = unit - a.unit_prefix[b];
+  // Windows of the sequence, clamped to what its raw keys (inside the key
+  // tensor) and its output rows (inside the output) allow.
+  const int64_t r0 = a.cu_raw[b], c0 = a.cu_comp[b];
+  int64_t raw_len = (a.cu_raw[b + 1] < a.T_raw ? a.cu_raw[b + 1] : a.T_raw) - r0;
+  int64_t lk = a.cu_comp[b + 1] - c0;
+  const int64_t lk_raw = raw_len >= 2 * kStride ? (raw_len - 2 * kStride) / kStride + 1 : 0;
+  lk = lk < lk_raw ? lk : lk_raw;
+  lk = lk < a.T_comp - c0 ? lk : a.T_comp - c0;
+  if (r0 < 0 || c0 < 0) return;
+  const int64_t j_lo = (run * groups + grp) * a.per_group;
+  int64_t j_hi = j_lo + a.per_group;
+  j_hi = j_hi < lk ? j_hi : lk;
+  const __bf16* kb = a.k + r0 * a.k_st + h * a.k_sh + d0;
+  uint16_t* ob = a.out + (c0 * a.H + h) * a.D + d0;
+  for (int64_t j = j_lo; j < j_hi; ++j) {
+    float h0[8], h1[8];
+    window<kStride>(kb, a.k_st, j, h0, h1);
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = f32_to_bf16_bits((h0[2 * e] + h1[2 * e]) * a.inv_kernel);
+      const uint32_t hi = f32_to_bf16_bits((h0[2 * e + 1] + h1[2 * e + 1]) * a.inv_kernel);
+      pk[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<i32x4*>(ob + j * a.H * a.D) =
+        i32x4{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+  }
+}
+
+}  // namespace
+}  // namespace unum
+
+extern "C" int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                                  const int32_t* cu_seqlens_raw, const int32_t* cu_seqlens_comp,
+                                  const int32_t* unit_prefix, int64_t n_units, void* out,
+                                  int64_t B, int64_t T_raw, int64_t T_comp, int64_t H, int64_t D,
+                                  int32_t kernel_size, int32_t stride, int32_t windows_per_unit,
+                                  void* stream) {
+  using namespace unum;
+  clear_error();
+  UNUM_REQUIRE(B >= 0 && T_raw >= 0 && T_comp >= 0 && n_units >= 0 && H > 0 && D > 0,
+               "compress_keys: bad sizes (B=%lld T_comp=%lld units=%lld H=%lld D=%lld)",
+               (long long)B, (long long)T_comp, (long long)n_units, (long long)H, (long long)D);
+  UNUM_REQUIRE(kernel_size == 2 * stride && stride == 16,
+               "compress_keys: kernel_size=%d stride=%d (supported: 32 / 16)", kernel_size, stride);
+  UNUM_REQUIRE(D % 8 == 0 && H * (D / 8) <= kWave,
+               "compress_keys: H*D/8 = %lld must be at most 64 with D %% 8 == 0",
+               (long long)(H * (D / 8)));
+  UNUM_REQUIRE(windows_per_unit > 0, "compress_keys: windows_per_unit=%d", windows_per_unit);
+  if (T_comp == 0 || B == 0 || n_units == 0) return UNUM_OK;
+  UNUM_REQUIRE(k && out && cu_seqlens_raw && cu_seqlens_comp && unit_prefix,
+               "compress_keys: null pointer");
+  UNUM_REQUIRE((reinterpret_cast<uintptr_t>(k) & 15) == 0 && (k_stride_t % 8) == 0 &&
+                   (k_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "compress_keys: keys and output must be 16-byte aligned (strides %% 8 == 0)");
+  const int32_t groups = static_cast<int32_t>(kWave / (H * (D / 8)));
+  UNUM_REQUIRE(windows_per_unit % groups == 0,
+               "compress_keys: windows_per_unit=%d not a multiple of the %d lane groups",
+               windows_per_unit, groups);
+  const int64_t blocks = (n_units * kWave + 255) / 256;
+  UNUM_REQUIRE(blocks <= INT32_MAX, "compress_keys: too many units (%lld)", (long long)n_units);
+  CompressArgs a;
+  a.k = static_cast<const __bf16*>(k);
+  a.k_st = k_stride_t;
+  a.k_sh = k_stride_h;
+  a.cu_raw = cu_seqlens_raw;
+  a.cu_comp = cu_seqlens_comp;
+  a.unit_prefix = unit_prefix;
+  a.out = static_cast<uint16_t*>(out);
+  a.B = B;
+  a.n_units = n_units;
+  a.T_raw = T_raw;
+  a.T_comp = T_comp;
+  a.H = static_cast<int32_t>(H);
+  a.D = static_cast<int32_t>(D);
+  a.stride = stride;
+  a.per_group = windows_per_unit / groups;
+  a.inv_kernel = 1.0f / static_cast<float>(kernel_size);
+  hipLaunchKernelGGL(compress_keys_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("compress_keys");
+}
