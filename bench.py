@@ -41,7 +41,8 @@ def parse():
                     help="skip the CPU oracle timing (e.g. under a profiler)")
     ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
                                        "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
-                                       "compress_keys_cfg5", "copy"], default=None,
+                                       "compress_keys_cfg5", "stage1_maxpool",
+                                       "stage1_maxpool_cfg5", "copy"], default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -103,8 +104,9 @@ def main():
     import torch
 
     from unum_ops_amd import workloads
-    from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
     from unum_ops_amd.compression import CompressionPlan, compress_keys
+    from unum_ops_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_maxpool,
+                                        max_pooling_1d_varlen)
     from unum_ops_amd.pipeline import maxpool_topk
     from unum_ops_amd.sparse_kernel_extension import get_block_table
 
@@ -152,6 +154,16 @@ def main():
 
     plan5 = CompressionPlan(torch.tensor([0, 135168]), 2, 128, dev)
 
+    def op_stage1_maxpool():
+        return infllmv2_attn_stage1_maxpool(s1g["q"], s1g["k"], s1g["cu_seqlens_q"],
+                                            s1g["cu_seqlens_k"], 8192,
+                                            max_seqlen_k=s1g["max_seqlen_k"], causal=True)
+
+    def op_stage1_maxpool_cfg5():
+        return infllmv2_attn_stage1_maxpool(c5["q"], c5["k"], c5["cu_q"], c5["cu_k"],
+                                            c5["max_context_len"],
+                                            max_seqlen_k=c5["max_seqlen_k"], causal=True)
+
     def op_compress_cfg5():
         return compress_keys(c5["raw"], c5["cu_raw"], plan=plan5)
 
@@ -161,7 +173,8 @@ def main():
     # compression of cfg5's raw keys.
     extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5),
              ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5),
-             ("compress_keys_cfg5", op_compress_cfg5)]
+             ("compress_keys_cfg5", op_compress_cfg5), ("stage1_maxpool", op_stage1_maxpool),
+             ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -258,6 +271,15 @@ def main():
                                config=("cfg2 input" if name == "maxpool_topk" else "cfg5 scores")
                                + " -> top-64 block ids int32 [2, T, 64]")
 
+    for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5")):
+        if name in per_op and src in comps:
+            flop = comps[src]["flop"]
+            t = per_op[name] * 1e-3
+            comps[name] = dict(us=per_op[name] * 1e3, tflops=flop / t / 1e12,
+                               pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                               config=f"{src} fused with the max-pool: pooled fp32 "
+                                      "[Hkv, Tq, NB] only (scores not stored); rows of at "
+                                      "most 512 keys (cfg3) run the two kernels")
     if "compress_keys_cfg5" in per_op:
         nbytes = 2 * 135168 * 2 * 128 + 2 * 8447 * 2 * 128
         t = per_op["compress_keys_cfg5"] * 1e-3

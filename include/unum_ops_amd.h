@@ -89,6 +89,28 @@ int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t 
                                                  int64_t max_seqlen_k);
 
 /*
+ * Stage 1 with the max-pool fused into it.  No single reference function: it
+ * equals max_pooling_1d_varlen (max_pooling_1d_varlen.py:127-183; block 64,
+ * stride 16, cache_lens 0) applied to infllmv2_attn_stage1's fp32 scores with
+ * max_seqlen_q = 16 * out_cols, i.e. each row pooled in place -- the way the
+ * selection pipeline chains the two -- without the scores going through HBM.
+ *
+ *   scores  optional fp32 [Hkv, Tq, out_cols] (NULL: not written)
+ *   pooled  fp32 [Hkv, Tq, num_blocks]
+ * Other arguments as unum_infllmv2_attn_stage1 and unum_max_pooling_1d_varlen.
+ * Only the MFMA paths (G = 16, D = 128, 16-byte aligned q/k, scale > 0) are
+ * fused; other shapes return UNUM_ERR_UNSUPPORTED.
+ */
+int unum_infllmv2_attn_stage1_maxpool(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                      const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                      void* scores, float* pooled, int64_t B, int64_t Tq,
+                                      int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t max_seqlen_k, int64_t out_cols, float scale,
+                                      int32_t causal, int64_t num_blocks, int32_t local_blocks,
+                                      int32_t init_blocks, void* stream);
+
+/*
  * Varlen 1-D max-pool of compressed-block scores, replacing
  * max_pooling_1d_varlen (max_pooling_1d_varlen.py:127-183, kernel :33-124).
  *

@@ -43,6 +43,17 @@ struct Stage1Args {
   int32_t causal;
 };
 
+// Fused max-pool (kernels instantiated with kPool): pooled [Hkv, Tq, nb] fp32
+// of each row's own scores, as max_pooling_1d_varlen computes it with block
+// 64 / stride 16 and a flat row stride of out_cols.  Kept apart from
+// Stage1Args so the unfused kernels do not carry its fields.
+struct Stage1Pool {
+  float* pooled;
+  int32_t nb;
+  int32_t init_blocks, local_blocks;
+  int32_t write_scores;     // 0: the scores are not stored
+};
+
 __device__ __forceinline__ int32_t tdiv16(int32_t a) {  // truncating a / 16
   return a / 16;  // C++ integer division truncates toward zero
 }
@@ -118,6 +129,70 @@ __device__ __forceinline__ float group_sum4(float v) {  // across the 4 lane gro
   v += __shfl_xor(v, 16);
   v += __shfl_xor(v, 32);
   return v;
+}
+
+// Raw buffer resources: loads past `bytes` read 0 and stores past it are
+// dropped by the hardware range check.
+constexpr uint32_t kBufferFlags = 0x00020000;  // gfx9 raw buffer resource word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           static_cast<int>(kBufferFlags));
+}
+constexpr int kDropOffset = 0x7fffffff;  // an offset past every range: the store is dropped
+
+// Buffer stores take every offset in the vector operand: the hardware range
+// check covers it, not the scalar offset.  Row stores use one descriptor per
+// row, so the range also stops a row's last chunk at the row end.
+template <typename OutT>
+__device__ __forceinline__ void buffer_store_out(__amdgpu_buffer_rsrc_t r, int off, float v) {
+  if constexpr (sizeof(OutT) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v), r, off, 0, 0);
+  }
+}
+
+// Fused max-pool of one 64-key quad of a row's scores (lane = key - key0):
+// block n = key0/4 + lane/4 takes the taps 4n-1 .. 4n+3 that lie below lk
+// (the -1 tap is the previous quad's last key, `carry`); +inf when forced
+// (n < init_blocks or n <= ob <= n + local_blocks), -inf when no tap is
+// present -- max_pooling_1d_varlen with block 64 / stride 16.  Lanes 4i store
+// block i; `carry` becomes this quad's last tap.
+__device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_rsrc_t prs,
+                                          int32_t key0, int32_t lk, int32_t ob, float o,
+                                          float& carry) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const float x = key0 + lane < lk ? o : -INFINITY;
+  float m = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+  float left = __shfl_up(x, 1);
+  left = lane == 0 ? carry : left;
+  const int32_t n = (key0 >> 2) + (lane >> 2);
+  const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
+  const float blk = force ? INFINITY : fmaxf(m, left);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(blk), prs,
+                                        (lane & 3) == 0 ? n * 4 : kDropOffset, 0, 0);
+  carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), kWave - 1));
+}
+
+// Pooled blocks past the computed columns (first = the first such block):
+// only the first can still hold a tap (the last column, via `carry`).
+__device__ __forceinline__ void pool_tail(const Stage1Pool& a, __amdgpu_buffer_rsrc_t prs,
+                                          int32_t first, int32_t ob, float carry) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int64_t n = first + lane; n < a.nb; n += kWave) {
+    const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
+    const float v = force ? INFINITY : (n == first ? carry : -INFINITY);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), prs, static_cast<int>(n * 4), 0, 0);
+  }
+}
+
+
+
+// Pooled row of a token outside every sequence: no taps, block of the token 0.
+__device__ __forceinline__ void orphan_pool_row(const Stage1Pool& p, int64_t row) {
+  pool_tail(p, make_rsrc(p.pooled + row * p.nb, static_cast<uint32_t>(p.nb * 4)), 0, 0, -INFINITY);
 }
 
 // ---------------------------------------------------------------- MFMA path
@@ -425,20 +500,6 @@ __device__ __forceinline__ float grp_sum16(float v) {
   v += dpp_f<0x141>(v);
   v += dpp_f<0x140>(v);
   return v;
-}
-
-// Per-lane head partials of four tiles (pa..pd) -> lane group u holds the full
-// head sum of tile u for key l%16 (two exchange steps instead of four
-// all-reduces).
-__device__ __forceinline__ float head_sum_quad(float pa, float pb, float pc, float pd) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const bool hi32 = lane >= 32;
-  const float send0 = hi32 ? pa : pc, send1 = hi32 ? pb : pd;
-  const float keep0 = hi32 ? pc : pa, keep1 = hi32 ? pd : pb;
-  const float x = keep0 + __shfl_xor(send0, 32);
-  const float y = keep1 + __shfl_xor(send1, 32);
-  const bool odd = (lane & 16) != 0;
-  return (odd ? y : x) + __shfl_xor(odd ? x : y, 16);
 }
 
 enum SegKind { kSeq = 0, kOrphan = 1, kSkip = 2 };
@@ -779,7 +840,6 @@ __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args
 // so each chunk issues the same memory operations and waits stay exact.
 constexpr int kStChunkTiles = 16;                          // 256 keys
 constexpr int kStChunkUnits = kStChunkTiles * 4 * kWave;   // 4096 bf16x8 units: 64 KiB
-constexpr uint32_t kBufferFlags = 0x00020000;              // gfx9 raw buffer resource word 3
 constexpr float kStLimit = 18446744073709551616.f;         // 2^64
 #ifndef UNUM_STREAM_TW
 #define UNUM_STREAM_TW 2
@@ -791,11 +851,6 @@ constexpr int kStTokensPerWave = UNUM_STREAM_TW;  // tokens sharing each K fragm
 constexpr int kStWaves = UNUM_STREAM_WAVES;       // waves per workgroup
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
-                                           static_cast<int>(kBufferFlags));
-}
 
 // Issue the loads of chunk `ch` (keys 256*ch ..) of the piece's K block; keys
 // past the valid range read as zero (buffer range check).
@@ -855,8 +910,9 @@ __device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const F
   }
 }
 
-template <typename OutT, int W, int TW>
-__global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, int64_t n_rows) {
+template <typename OutT, int W, int TW, bool kPool>
+__global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
+                                                                 int64_t n_rows) {
   __shared__ bf16x8 kbuf[2][kStChunkUnits];
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
   // per-token rows and store descriptors in scalar registers.
@@ -888,8 +944,11 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, i
       for (int64_t j = wave; j < n; j += W) {
         const int64_t rel = r + j - sg.rlo;
         const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
-        if (g < a.Hkv && t < a.Tq)
-          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+        if (g < a.Hkv && t < a.Tq) {
+          if (!kPool || pp.write_scores)
+            zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+          if constexpr (kPool) orphan_pool_row(pp, g * a.Tq + t);
+        }
       }
       r = sg.end;
       continue;
@@ -933,6 +992,9 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, i
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, k_bytes);
 
     float nb[TW][4];  // pass-2 bias: p = exp2(c*s + nb)
+    [[maybe_unused]] float carry_out[TW];  // fused pool: each token's last tap so far
+#pragma unroll
+    for (int k = 0; k < TW; ++k) carry_out[k] = -INFINITY;
     for (int pass = 0; pass < 2 && nch > 0; ++pass) {
       float mref[TW][4], mc[TW][4], l[TW][4];
 #pragma unroll
@@ -943,12 +1005,18 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, i
           mc[k][rr] = 0.f;
           l[k][rr] = 0.f;
         }
-      OutT* orow[TW];
+      // Per-token row descriptors: their ranges drop stores past the row
+      // end, and every store of a token this wave computes but does not own
+      // (and the scores when they are not wanted).
       __amdgpu_buffer_rsrc_t orsrc[TW];
+      [[maybe_unused]] __amdgpu_buffer_rsrc_t prsrc[TW];
 #pragma unroll
       for (int k = 0; k < TW; ++k) {
-        orow[k] = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k]) * a.out_cols;
-        orsrc[k] = make_rsrc(orow[k], own[k] ? row_bytes : 0u);
+        const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k];
+        orsrc[k] = make_rsrc(static_cast<OutT*>(a.out) + row * a.out_cols,
+                             own[k] && (!kPool || pp.write_scores) ? row_bytes : 0u);
+        if constexpr (kPool)
+          prsrc[k] = make_rsrc(pp.pooled + row * pp.nb, own[k] ? static_cast<uint32_t>(pp.nb * 4) : 0u);
       }
       u32x4 stage[kPer];
       __syncthreads();  // the previous user of kbuf is done
@@ -1083,12 +1151,8 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, i
               f32x4 o = {0.f, 0.f, 0.f, 0.f};
               o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, o, 0, 0, 0);
               o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, o, 0, 0, 0);
-              const int off = (key0 + lane) * static_cast<int>(sizeof(OutT));
-              if constexpr (sizeof(OutT) == 4) {
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o.x), orsrc[k], off, 0, 0);
-              } else {
-                __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(o.x), orsrc[k], off, 0, 0);
-              }
+              buffer_store_out<OutT>(orsrc[k], (key0 + lane) * static_cast<int>(sizeof(OutT)), o.x);
+              if constexpr (kPool) pool_quad(pp, prsrc[k], key0, sg.lk, lq[k] >> 6, o.x, carry_out[k]);
             }
           }
         }
@@ -1113,8 +1177,15 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, i
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
       if (own[k]) {
-        OutT* orow = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k]) * a.out_cols;
-        zero_row_vec<OutT>(orow, static_cast<int64_t>(nch) * kStChunkTiles * 16, a.out_cols);
+        const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k];
+        const int64_t done = static_cast<int64_t>(nch) * kStChunkTiles * 16;
+        if (!kPool || pp.write_scores)
+          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + row * a.out_cols, done, a.out_cols);
+        if constexpr (kPool) {
+          // The last streamed column's tap is carried only when a chunk ran.
+          pool_tail(pp, make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)),
+                    static_cast<int32_t>(done / 4), lq[k] >> 6, nch > 0 ? carry_out[k] : -INFINITY);
+        }
       }
     }
     r = sg.end;
@@ -1134,37 +1205,59 @@ int num_cus() {
   return cached[dev];
 }
 
+enum Stage1Path { kPathLds, kPathStream, kPathRowMfma, kPathGeneric };
+
 template <typename OutT>
-int launch_stage1(const Stage1Args& a, hipStream_t s) {
+Stage1Path stage1_path(const Stage1Args& a) {
   const bool aligned = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(a.k) & 15) == 0 && (a.q_st % 8) == 0 &&
                        (a.q_sh % 8) == 0 && (a.k_st % 8) == 0 && (a.k_sh % 8) == 0;
-  if (a.G == kG && a.D == kD && aligned && a.out_cols <= kLdsTiles * 16 &&
-      (a.out_cols % 64) == 0 && a.scale_log2 > 0.f) {
-    const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
+  const bool mfma = a.G == kG && a.D == kD && aligned;
+  if (mfma && a.out_cols <= kLdsTiles * 16 && (a.out_cols % 64) == 0 && a.scale_log2 > 0.f)
+    return kPathLds;
+  if (mfma && a.scale_log2 > 0.f && a.k_st >= kD &&
+      (a.out_cols + kStChunkTiles * 16) * a.k_st * 2 < (int64_t{1} << 31) &&
+      a.out_cols * static_cast<int64_t>(sizeof(OutT)) < (int64_t{1} << 31))
+    return kPathStream;
+  return mfma ? kPathRowMfma : kPathGeneric;
+}
+
+template <typename OutT, bool kPool>
+int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, hipStream_t s) {
+  const Stage1Path path = stage1_path<OutT>(a);
+  // The pool is fused into the K-streaming kernel only: in the LDS-resident
+  // kernel (rows of at most 512 keys) the extra state pushed the row's
+  // registers into spills, and the two separate kernels measured faster.
+  if (kPool && path != kPathStream)
+    UNUM_FAIL(UNUM_ERR_UNSUPPORTED,
+              "infllmv2_attn_stage1_maxpool: fused only for rows over 512 keys with G=16, "
+              "D=128, 16-byte aligned q/k and a positive scale (got G=%d, D=%d, %lld columns)",
+              a.G, a.D, (long long)a.out_cols);
+  const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
+  if constexpr (kPool) {
+    constexpr int kTW = kStTokensPerWave;
+    const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, true>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp, n_rows);
+  } else if (path == kPathLds) {
     int64_t grid = (n_rows + kLdsWaves - 1) / kLdsWaves;
     const int64_t cus = num_cus();
     grid = grid < cus ? grid : cus;
     const dim3 g(static_cast<unsigned>(grid)), b(kLdsWaves * kWave);
     switch (a.out_cols / 64) {
-      case 1: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 1>), g, b, 0, s, a, n_rows); break;
-      case 2: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 2>), g, b, 0, s, a, n_rows); break;
-      case 3: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 3>), g, b, 0, s, a, n_rows); break;
-      case 4: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 4>), g, b, 0, s, a, n_rows); break;
-      case 5: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 5>), g, b, 0, s, a, n_rows); break;
-      case 6: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 6>), g, b, 0, s, a, n_rows); break;
-      case 7: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 7>), g, b, 0, s, a, n_rows); break;
+#define UNUM_LDS_CASE(N) \
+      case N: hipLaunchKernelGGL((stage1_lds_kernel<OutT, N>), g, b, 0, s, a, n_rows); break;
+      UNUM_LDS_CASE(1) UNUM_LDS_CASE(2) UNUM_LDS_CASE(3) UNUM_LDS_CASE(4)
+      UNUM_LDS_CASE(5) UNUM_LDS_CASE(6) UNUM_LDS_CASE(7)
+#undef UNUM_LDS_CASE
       default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
     }
-  } else if (a.G == kG && a.D == kD && aligned && a.scale_log2 > 0.f && a.k_st >= kD &&
-             (a.out_cols + kStChunkTiles * 16) * a.k_st * 2 < (int64_t{1} << 31) &&
-             a.out_cols * static_cast<int64_t>(sizeof(OutT)) < (int64_t{1} << 31)) {
+  } else if (path == kPathStream) {
     constexpr int kTW = kStTokensPerWave;
-    const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
     const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
-    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kStWaves * kWave), 0, s, a, n_rows);
-  } else if (a.G == kG && a.D == kD && aligned) {
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp, n_rows);
+  } else if (path == kPathRowMfma) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
     hipLaunchKernelGGL(stage1_mfma_kernel<OutT>, grid, dim3(256), 0, s, a);
   } else {
@@ -1185,34 +1278,29 @@ extern "C" int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t, int64_t, in
   return 0;
 }
 
-extern "C" int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_stride_h,
-                                         const void* k, int64_t k_stride_t, int64_t k_stride_h,
-                                         const int32_t* cu_seqlens_q,
-                                         const int32_t* cu_seqlens_k, void* out,
-                                         int32_t out_dtype, int64_t B, int64_t Tq, int64_t Tk,
-                                         int64_t Hq, int64_t Hkv, int64_t D,
-                                         int64_t max_seqlen_k, int64_t out_cols, float scale,
-                                         int32_t causal, void* workspace,
-                                         int64_t workspace_bytes, void* stream) {
-  using namespace unum;
-  (void)workspace;
-  (void)workspace_bytes;
-  clear_error();
+namespace unum {
+namespace {
+// Validation and argument packing shared by both entry points.
+int stage1_args(Stage1Args& a, const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, void* out, int64_t B,
+                int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
+                int64_t max_seqlen_k, int64_t out_cols, float scale, int32_t causal,
+                const char* op) {
   UNUM_REQUIRE(B >= 0 && Tq >= 0 && Tk >= 0 && Hq > 0 && Hkv > 0 && D > 0 && out_cols >= 0,
-               "infllmv2_attn_stage1: bad sizes (B=%lld Tq=%lld Tk=%lld Hq=%lld Hkv=%lld D=%lld)",
+               "%s: bad sizes (B=%lld Tq=%lld Tk=%lld Hq=%lld Hkv=%lld D=%lld)", op,
                (long long)B, (long long)Tq, (long long)Tk, (long long)Hq, (long long)Hkv,
                (long long)D);
-  UNUM_REQUIRE(Hq % Hkv == 0, "infllmv2_attn_stage1: Hq=%lld not a multiple of Hkv=%lld",
-               (long long)Hq, (long long)Hkv);
-  UNUM_REQUIRE(max_seqlen_k <= out_cols,
-               "infllmv2_attn_stage1: max_seqlen_k=%lld exceeds the %lld output columns",
-               (long long)max_seqlen_k, (long long)out_cols);
-  if (Tq == 0 || out_cols == 0) return UNUM_OK;
-  UNUM_REQUIRE(q && k && out && cu_seqlens_q && cu_seqlens_k, "infllmv2_attn_stage1: null pointer");
-  UNUM_REQUIRE(B >= 1, "infllmv2_attn_stage1: cu_seqlens must hold at least 2 entries");
-  UNUM_REQUIRE(Tk >= 1, "infllmv2_attn_stage1: empty k");
-  UNUM_REQUIRE(Tq <= INT32_MAX && Hkv <= 65535, "infllmv2_attn_stage1: size exceeds grid");
-  Stage1Args a;
+  UNUM_REQUIRE(Hq % Hkv == 0, "%s: Hq=%lld not a multiple of Hkv=%lld", op, (long long)Hq,
+               (long long)Hkv);
+  UNUM_REQUIRE(max_seqlen_k <= out_cols, "%s: max_seqlen_k=%lld exceeds the %lld output columns",
+               op, (long long)max_seqlen_k, (long long)out_cols);
+  a = Stage1Args{};
+  if (Tq == 0 || out_cols == 0) return 1;  // nothing to launch
+  UNUM_REQUIRE(q && k && cu_seqlens_q && cu_seqlens_k, "%s: null pointer", op);
+  UNUM_REQUIRE(B >= 1, "%s: cu_seqlens must hold at least 2 entries", op);
+  UNUM_REQUIRE(Tk >= 1, "%s: empty k", op);
+  UNUM_REQUIRE(Tq <= INT32_MAX && Hkv <= 65535, "%s: size exceeds grid", op);
   a.q = static_cast<const __bf16*>(q);
   a.q_st = q_stride_t;
   a.q_sh = q_stride_h;
@@ -1232,11 +1320,64 @@ extern "C" int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int6
   a.out_cols = out_cols;
   a.scale_log2 = scale * kLog2e;
   a.causal = causal;
+  return 0;
+}
+}  // namespace
+}  // namespace unum
+
+extern "C" int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                         const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                                         const int32_t* cu_seqlens_q,
+                                         const int32_t* cu_seqlens_k, void* out,
+                                         int32_t out_dtype, int64_t B, int64_t Tq, int64_t Tk,
+                                         int64_t Hq, int64_t Hkv, int64_t D,
+                                         int64_t max_seqlen_k, int64_t out_cols, float scale,
+                                         int32_t causal, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  using namespace unum;
+  (void)workspace;
+  (void)workspace_bytes;
+  clear_error();
+  Stage1Args a;
+  const int st = stage1_args(a, q, q_stride_t, q_stride_h, k, k_stride_t, k_stride_h,
+                             cu_seqlens_q, cu_seqlens_k, out, B, Tq, Tk, Hq, Hkv, D,
+                             max_seqlen_k, out_cols, scale, causal, "infllmv2_attn_stage1");
+  if (st != 0) return st < 0 ? st : UNUM_OK;
+  UNUM_REQUIRE(out, "infllmv2_attn_stage1: null output");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
-    case UNUM_DTYPE_F32: return launch_stage1<float>(a, s);
-    case UNUM_DTYPE_BF16: return launch_stage1<uint16_t>(a, s);
+    case UNUM_DTYPE_F32: return launch_stage1<float, false>(a, Stage1Pool{}, s);
+    case UNUM_DTYPE_BF16: return launch_stage1<uint16_t, false>(a, Stage1Pool{}, s);
     default:
       UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "infllmv2_attn_stage1: unsupported out dtype %d", out_dtype);
   }
+}
+
+extern "C" int unum_infllmv2_attn_stage1_maxpool(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t,
+    int64_t k_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, void* scores,
+    float* pooled, int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
+    int64_t max_seqlen_k, int64_t out_cols, float scale, int32_t causal, int64_t num_blocks,
+    int32_t local_blocks, int32_t init_blocks, void* stream) {
+  using namespace unum;
+  clear_error();
+  const char* op = "infllmv2_attn_stage1_maxpool";
+  UNUM_REQUIRE(num_blocks >= 0, "%s: num_blocks=%lld", op, (long long)num_blocks);
+  UNUM_REQUIRE(num_blocks <= (int64_t{1} << 28) && out_cols <= (int64_t{1} << 28),
+               "%s: rows too long", op);
+  Stage1Args a;
+  const int st = stage1_args(a, q, q_stride_t, q_stride_h, k, k_stride_t, k_stride_h,
+                             cu_seqlens_q, cu_seqlens_k, scores, B, Tq, Tk, Hq, Hkv, D,
+                             max_seqlen_k, out_cols, scale, causal, op);
+  if (st < 0) return st;
+  if (Tq == 0 || num_blocks == 0) return UNUM_OK;
+  UNUM_REQUIRE(pooled, "%s: null pooled output", op);
+  UNUM_REQUIRE(out_cols > 0, "%s: out_cols must be positive", op);
+  Stage1Pool pp;
+  pp.pooled = pooled;
+  pp.nb = static_cast<int32_t>(num_blocks);
+  pp.init_blocks = init_blocks;
+  pp.local_blocks = local_blocks;
+  pp.write_scores = scores != nullptr;
+  return launch_stage1<float, true>(a, pp, static_cast<hipStream_t>(stream));
 }

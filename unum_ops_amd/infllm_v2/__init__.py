@@ -152,6 +152,96 @@ def max_pooling_1d_varlen(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seq
     return out
 
 
+def infllmv2_attn_stage1_maxpool(q, k, cu_seqlens_q, cu_seqlens_k, max_context_len,
+                                 max_seqlen_k=None, softmax_scale=None, causal=True,
+                                 local_blocks=1, init_blocks=1, block_size=64, stride=16,
+                                 return_scores=False):
+    """Pooled block scores ``[Hkv, total_q, ceil(max_context_len / 64)]`` (fp32).
+
+    Equal to ``max_pooling_1d_varlen(infllmv2_attn_stage1(q, k, None,
+    cu_seqlens_q, cu_seqlens_k, max_seqlen_k=..., causal=...), cu_seqlens_q,
+    cu_seqlens_k, zeros, max_seqlen_q=16 * Kp, max_context_len, local_blocks,
+    init_blocks)`` -- each row pooled in place, as the selection pipeline
+    chains the two ops -- computed in one kernel, so the fp32 scores only go
+    to HBM when ``return_scores`` asks for them (then ``(pooled, scores)``).
+    Shapes off the MFMA paths (G != 16, D != 128, ...) and ``block_size /
+    stride`` other than 64 / 16 run the two ops separately.
+    """
+    op = "infllmv2_attn_stage1_maxpool"
+    dev = require_gpu(op, q, k, cu_seqlens_q, cu_seqlens_k)
+    if block_size != 64 or stride != 16 or q.dim() != 3 or k.dim() != 3 \
+            or q.shape[1] != 16 * k.shape[1] or q.shape[2] != 128:
+        sc = infllmv2_attn_stage1(q, k, None, cu_seqlens_q, cu_seqlens_k,
+                                  max_seqlen_k=max_seqlen_k, softmax_scale=softmax_scale,
+                                  causal=causal)
+        batch = cu_seqlens_q.shape[0] - 1
+        pooled = max_pooling_1d_varlen(sc, cu_seqlens_q, cu_seqlens_k,
+                                       torch.zeros(max(batch, 1), dtype=torch.int32, device=dev),
+                                       max_seqlen_q=stride * sc.shape[-1],
+                                       max_context_len=max_context_len,
+                                       local_blocks=local_blocks, init_blocks=init_blocks,
+                                       block_size=block_size, stride=stride)
+        return (pooled, sc) if return_scores else pooled
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    if q.dtype != torch.bfloat16:
+        q = q.to(torch.bfloat16)
+    if k.dtype != torch.bfloat16:
+        k = k.to(torch.bfloat16)
+    if softmax_scale is None:
+        softmax_scale = q.shape[-1] ** (-0.5)
+    total_q, n_heads, head_dim = q.shape
+    total_k, n_kv_heads, _ = k.shape
+    batch = cu_seqlens_q.numel() - 1
+    cu_q = as_i32(cu_seqlens_q, "cu_seqlens_q", op)
+    cu_k = as_i32(cu_seqlens_k, "cu_seqlens_k", op)
+    if cu_k.numel() != batch + 1:
+        raise ValueError(f"{op}: cu_seqlens_k has {cu_k.numel()} entries, expected {batch + 1}")
+    if max_seqlen_k is None or as_int(max_seqlen_k, "max_seqlen_k", op) == 0:
+        max_seqlen_k = int((cu_k[1:] - cu_k[:-1]).max().item()) if batch > 0 else 0
+    max_seqlen_k = as_int(max_seqlen_k, "max_seqlen_k", op)
+    cols = round_multiple(max_seqlen_k, 128) if max_seqlen_k > 0 else 0
+    nb = math.ceil(as_int(max_context_len, "max_context_len", op) / block_size)
+    pooled = torch.empty(n_kv_heads, total_q, nb, device=dev, dtype=torch.float32)
+    scores = torch.empty(n_kv_heads, total_q, cols, device=dev, dtype=torch.float32) \
+        if return_scores else None
+    if cols == 0 or total_k == 0 or batch <= 0 or softmax_scale <= 0:
+        # No keys, or a scale the fused kernels do not take: the two ops.
+        return _unfused(q, k, cu_q, cu_k, max_seqlen_k, softmax_scale, causal, max_context_len,
+                        local_blocks, init_blocks, return_scores, dev)
+    if pooled.numel() == 0:
+        return (pooled, scores) if return_scores else pooled
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.unum_infllmv2_attn_stage1_maxpool(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+            _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(scores), _lib.ptr(pooled),
+            batch, total_q, total_k, n_heads, n_kv_heads, head_dim, max_seqlen_k, cols,
+            float(softmax_scale), 1 if causal else 0, nb, int(local_blocks), int(init_blocks),
+            _lib.stream_ptr(dev))
+    if st == _lib.UNUM_ERR_UNSUPPORTED:
+        # a layout off the MFMA paths (e.g. unaligned q/k): the two ops take it
+        return _unfused(q, k, cu_q, cu_k, max_seqlen_k, softmax_scale, causal, max_context_len,
+                        local_blocks, init_blocks, return_scores, dev)
+    _lib.check(st, op)
+    return (pooled, scores) if return_scores else pooled
+
+
+def _unfused(q, k, cu_q, cu_k, max_seqlen_k, softmax_scale, causal, max_context_len,
+             local_blocks, init_blocks, return_scores, dev):
+    sc = infllmv2_attn_stage1(q, k, None, cu_q, cu_k, max_seqlen_k=max_seqlen_k,
+                              softmax_scale=softmax_scale, causal=causal)
+    batch = cu_q.numel() - 1
+    pooled = max_pooling_1d_varlen(sc, cu_q, cu_k,
+                                   torch.zeros(max(batch, 1), dtype=torch.int32, device=dev),
+                                   max_seqlen_q=16 * max(sc.shape[-1], 1),
+                                   max_context_len=max_context_len,
+                                   local_blocks=local_blocks, init_blocks=init_blocks)
+    return (pooled, sc) if return_scores else pooled
+
+
 # Names exported by the reference package (``src/unum_ops/infllm_v2/__init__.py``).
 infllmv2_attn_stage1_triton = infllmv2_attn_stage1
 infllmv2_attn_stage1_triton_v2 = infllmv2_attn_stage1
@@ -159,6 +249,7 @@ max_pooling_1d_varlen_ref_triton = max_pooling_1d_varlen
 
 __all__ = [
     "infllmv2_attn_stage1",
+    "infllmv2_attn_stage1_maxpool",
     "infllmv2_attn_stage1_triton",
     "infllmv2_attn_stage1_triton_v2",
     "max_pooling_1d_varlen",
