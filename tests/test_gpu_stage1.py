@@ -137,3 +137,26 @@ def test_cfg3_full_size_properties(dev):
         rows = list(range(0, 96)) + list(range(4000, 4096)) + list(range(8096, 8192))
         torch.testing.assert_close(out[:, qs + torch.tensor(rows)].cpu(), exp_b[:, rows],
                                    atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("boost", [4.0, 60.0])
+def test_later_keys_far_above_first_quad(boost, dev):
+    """Keys after the first 64 scaled up: the first quad's max is then far below
+    the row max (boost 60 pushes the per-head sums past 2^14, so those rows are
+    redone against their exact max; boost 4 stays on the first pass)."""
+    d = workloads.stage1_inputs([300, 77], [5000, 3000], seed=25)
+    k = d["k"].float()
+    cu_k = d["cu_seqlens_k"].tolist()
+    for b in range(2):
+        k[cu_k[b] + 64:cu_k[b + 1]] *= boost
+    d["k"] = k.to(torch.bfloat16)
+    _check(d, _run(d, dev))
+
+
+@pytest.mark.parametrize("q_lens", [[1], [3], [5], [7, 2], [129, 130, 131], [1023, 1]])
+def test_odd_lengths_and_pair_split(q_lens, dev):
+    """Odd sequence lengths (one token pair is split) and lengths that put a
+    workgroup boundary inside a pair."""
+    ctx = [16 * q + 900 for q in q_lens]
+    d = workloads.stage1_inputs(q_lens, ctx, seed=sum(q_lens))
+    _check(d, _run(d, dev))

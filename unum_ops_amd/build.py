@@ -37,9 +37,12 @@ HIP_FLAGS = [
 # Extra flags per source.  Stage 1 never produces or consumes a NaN (masked
 # scores are -inf and every exp argument is finite or -inf), so it is built
 # without NaN semantics: fmaxf then needs no quieting and the DPP lane moves
-# fold into the max/add of the cross-lane reductions.
+# fold into the max/add of the cross-lane reductions.  Its MFMA results are
+# read by the VALU right away (exponentials), so they are kept in VGPRs
+# (-amdgpu-mfma-vgpr-form); values that feed only MFMAs may then live in the
+# accumulation registers.
 FILE_FLAGS = {
-    "stage1.hip": ["-fno-honor-nans"],
+    "stage1.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -459,24 +459,11 @@ __global__ __launch_bounds__(64) void stage1_generic_kernel(Stage1Args a) {
   zero_tail<OutT>(orow, wr, a.out_cols);
 }
 
-// ----------------------------------------------------- LDS-resident K path
-// For sequences with at most kLdsTiles*16 = 512 compressed keys (the "32K"
-// prefill shapes), one persistent workgroup per CU keeps the whole compressed
-// K of one (sequence, group) in LDS -- 128 KiB, stored in MFMA B-fragment
-// order so a wave reads one 16x32 fragment with a single contiguous
-// ds_read_b128 -- and its eight waves each own whole (token, group) rows: the
-// row's score tiles stay in registers, the exact max is taken, and every
-// score is exponentiated once.
-//
-// Work split: the (group, token) rows of the batch are ordered by sequence,
-// then group, then token in zig-zag order (0, L-1, 1, L-2, ...), and each
-// workgroup takes one contiguous range of that order.  A range therefore
-// touches one or two (sequence, group) K blocks -- loaded once -- and its
-// causal work (which grows linearly with the token position) is balanced,
-// since consecutive zig-zag rows pair a short prefix with a long one.  Inside
-// a workgroup, wave w takes the row pairs (2w, 2w+1), (2w+16, 2w+17), ... of
-// a segment and prefetches the next row's query fragment while computing the
-// current one.
+// ------------------------------- row segments, shared by the workgroup paths
+// Rows (group, token) of the batch in the order sequence, group, token
+// zig-zag; a workgroup's contiguous range of that order is cut into segments
+// of one (sequence, group) each (or of tokens outside every sequence).  The
+// LDS-resident kernel that walks them is further below.
 constexpr int kLdsWaves = 8;
 constexpr int kLdsTiles = 32;                    // 512 keys
 constexpr int kLdsUnits = kLdsTiles * 4 * kWave; // bf16x8 units: 128 KiB
@@ -576,37 +563,6 @@ __device__ __forceinline__ int64_t zigzag(int64_t k, int64_t L) {
   return (k & 1) ? (L - 1 - (k >> 1)) : (k >> 1);
 }
 
-// K block (keys [0, 16*ntl), zero beyond lk) -> LDS in fragment order:
-// unit ((jt*4 + c)*64 + l) = k[ks + 16*jt + l%16][g][32*c + 8*(l/16) .. +8].
-// Each thread issues its (up to) 16 loads before writing any of them.
-__device__ __forceinline__ void load_k_block(const Stage1Args& a, bf16x8* kt, const Segment& sg,
-                                             int ntl) {
-  constexpr int kThreads = kLdsWaves * kWave;
-  constexpr int kPer = kLdsUnits / kThreads;  // 16
-  // An opaque copy of the thread index keeps the per-unit addresses from
-  // being hoisted out of the segment loop (and spilled) by the compiler.
-  int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
-  const int units = ntl * 4 * kWave;
-  const __bf16* kb = a.k + static_cast<int64_t>(sg.ks) * a.k_st + static_cast<int64_t>(sg.g) * a.k_sh;
-  const int64_t keys_ok = sg.lk < a.Tk - sg.ks ? sg.lk : a.Tk - sg.ks;  // keys inside k
-  bf16x8 v[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int u = tid + i * kThreads;
-    const int jt = u >> 8, cc = (u >> 6) & 3, l = u & 63;
-    const int key = 16 * jt + (l & 15);
-    v[i] = bf16x8{};
-    if (u < units && key < keys_ok && sg.ks + key >= 0)
-      v[i] = *reinterpret_cast<const bf16x8*>(kb + key * a.k_st + 32 * cc + 8 * (l >> 4));
-  }
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int u = tid + i * kThreads;
-    if (u < units) kt[u] = v[i];
-  }
-}
-
 template <typename OutT>
 __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t cols) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -618,201 +574,6 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
     }
   }
   zero_tail<OutT>(orow, from, cols);
-}
-
-// One (token, group) row with the whole key block in LDS.  kOutQ = out_cols/64
-// is a compile-time count: the row is written by exactly kOutQ 64-column
-// stores (computed chunks, then zeros), so the number of memory operations
-// between one row's query prefetch and its use is known to the compiler and
-// the wait before the next row covers only what it must.
-template <typename OutT, int kOutQ>
-__device__ __forceinline__ void lds_row(const Stage1Args& a, const bf16x8* kt, const Segment& sg,
-                                        int64_t t, int32_t lq, const Frag& qf) {
-  const int lane = threadIdx.x & (kWave - 1);
-  OutT* orow = static_cast<OutT*>(a.out) + (static_cast<int64_t>(sg.g) * a.Tq + t) * a.out_cols;
-  int32_t vis = sg.lk;
-  if (a.causal) {
-    vis = tdiv16(lq - 15) + sg.lk - tdiv16(sg.lq_len - 16 + 1);
-    vis = vis < 0 ? 0 : (vis > sg.lk ? sg.lk : vis);
-  }
-  vis = vis < 64 * kOutQ ? vis : 64 * kOutQ;  // keys past the output row are not written
-  vis = __builtin_amdgcn_readfirstlane(vis);   // wave-uniform: scalar branches below
-  const int nq = (vis + 63) >> 6;              // 64-key quads; 0 when nothing is visible
-  const float c = a.scale_log2;                // > 0 on this path
-  const bf16x8* kl = kt + lane;
-
-  // Scores of a quad (four 16-key tiles): the four tiles' accumulation chains
-  // are interleaved over the four K = 32 steps, and the next step's four
-  // B fragments are read from LDS while the current step's MFMAs run.
-  f32x4 s[4 * kOutQ];
-#pragma unroll
-  for (int qd = 0; qd < kOutQ; ++qd) {
-    if (qd < nq) {
-      const bf16x8* kq = kl + qd * 16 * kWave;  // fragment (u, cc) at kq[(4u + cc) * 64]
-      f32x4 acc[4];
-      bf16x8 cur[4], nxt[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-        cur[u] = kq[(4 * u + 0) * kWave];
-      }
-#pragma unroll
-      for (int cc = 0; cc < kD / 32; ++cc) {
-        if (cc + 1 < kD / 32) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) nxt[u] = kq[(4 * u + cc + 1) * kWave];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf.v[cc], cur[u], acc[u], 0, 0, 0);
-        if (cc + 1 < kD / 32) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) s[4 * qd + u] = acc[u];
-    }
-  }
-  // Max over the visible raw scores (scale > 0 keeps the order).  Only the
-  // last computed quad holds keys >= vis, so only it is masked; masked scores
-  // are -inf and exponentiate to 0 below.
-  float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-  for (int qd = 0; qd < kOutQ; ++qd) {
-    if (qd < nq) {
-      if (qd == nq - 1) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const bool ok = 64 * qd + 16 * u + (lane & 15) < vis;
-          const int jt = 4 * qd + u;
-          s[jt].x = ok ? s[jt].x : -INFINITY;
-          s[jt].y = ok ? s[jt].y : -INFINITY;
-          s[jt].z = ok ? s[jt].z : -INFINITY;
-          s[jt].w = ok ? s[jt].w : -INFINITY;
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int jt = 4 * qd + u;
-        m[0] = fmaxf(m[0], s[jt].x);
-        m[1] = fmaxf(m[1], s[jt].y);
-        m[2] = fmaxf(m[2], s[jt].z);
-        m[3] = fmaxf(m[3], s[jt].w);
-      }
-    }
-  }
-  // p = exp2(c*s - c*max): one fma and one exp per score.
-  float mc[4], l[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    mc[r] = -c * grp_max16(m[r]);
-    l[r] = 0.f;
-  }
-#pragma unroll
-  for (int qd = 0; qd < kOutQ; ++qd) {
-    if (qd < nq) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int jt = 4 * qd + u;
-        s[jt].x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].x, c, mc[0]));
-        s[jt].y = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].y, c, mc[1]));
-        s[jt].z = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].z, c, mc[2]));
-        s[jt].w = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt].w, c, mc[3]));
-        l[0] += s[jt].x;
-        l[1] += s[jt].y;
-        l[2] += s[jt].z;
-        l[3] += s[jt].w;
-      }
-    }
-  }
-  // Normalise and sum over the 16 heads on the matrix core: for tiles u of a
-  // quad, B = the tile's exponentials as f16 (lane (key n, group g) holds
-  // heads 4g..4g+3 -- the accumulator layout of the score MFMA is the B
-  // layout with heads as the reduction index), A = 1/l of those heads placed
-  // on rows 4u..4u+3.  Two K = 32 MFMAs (tiles 0,1 then 2,3, accumulated)
-  // leave every lane of group u holding the output of tile u for key l%16,
-  // i.e. the quad's 64 outputs in lane order.
-  f16x8 wa, wb;  // A operands: tiles (0,1) and (2,3)
-  {
-    float inv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) inv[r] = __builtin_amdgcn_rcpf(grp_sum16(l[r]));
-    const int m = lane & 15;  // A row of this lane
-    const _Float16 h0 = static_cast<_Float16>(inv[0]), h1 = static_cast<_Float16>(inv[1]);
-    const _Float16 h2 = static_cast<_Float16>(inv[2]), h3 = static_cast<_Float16>(inv[3]);
-    const _Float16 z = static_cast<_Float16>(0.f);
-    const bool lo_a = m < 4, hi_a = m >= 4 && m < 8, lo_b = m >= 8 && m < 12, hi_b = m >= 12;
-    wa = f16x8{lo_a ? h0 : z, lo_a ? h1 : z, lo_a ? h2 : z, lo_a ? h3 : z,
-               hi_a ? h0 : z, hi_a ? h1 : z, hi_a ? h2 : z, hi_a ? h3 : z};
-    wb = f16x8{lo_b ? h0 : z, lo_b ? h1 : z, lo_b ? h2 : z, lo_b ? h3 : z,
-               hi_b ? h0 : z, hi_b ? h1 : z, hi_b ? h2 : z, hi_b ? h3 : z};
-  }
-#pragma unroll
-  for (int qd = 0; qd < kOutQ; ++qd) {
-    float o = 0.f;
-    if (qd < nq) {
-      const f32x4* e = s + 4 * qd;
-      const f16x8 b01 = f16x8{static_cast<_Float16>(e[0].x), static_cast<_Float16>(e[0].y),
-                              static_cast<_Float16>(e[0].z), static_cast<_Float16>(e[0].w),
-                              static_cast<_Float16>(e[1].x), static_cast<_Float16>(e[1].y),
-                              static_cast<_Float16>(e[1].z), static_cast<_Float16>(e[1].w)};
-      const f16x8 b23 = f16x8{static_cast<_Float16>(e[2].x), static_cast<_Float16>(e[2].y),
-                              static_cast<_Float16>(e[2].z), static_cast<_Float16>(e[2].w),
-                              static_cast<_Float16>(e[3].x), static_cast<_Float16>(e[3].y),
-                              static_cast<_Float16>(e[3].z), static_cast<_Float16>(e[3].w)};
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, acc, 0, 0, 0);
-      o = acc.x;
-    }
-    store_out<OutT>(orow + 64 * qd + lane, o);
-  }
-}
-
-template <typename OutT, int kOutQ>
-__global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
-  __shared__ bf16x8 kt[kLdsUnits];
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int64_t r_begin = n_rows * blockIdx.x / gridDim.x;
-  const int64_t r_end = n_rows * (blockIdx.x + 1) / gridDim.x;
-  for (int64_t r = r_begin; r < r_end;) {
-    const Segment sg = find_segment(a, r, r_end);
-    const int64_t n = sg.end - r;
-    __syncthreads();  // the previous segment is done with kt
-    if (sg.kind == kSeq && sg.lk > 0) {
-      int ntl = 4 * ((sg.lk + 63) >> 6);
-      ntl = ntl < 4 * kOutQ ? ntl : 4 * kOutQ;
-      load_k_block(a, kt, sg, ntl);
-    }
-    __syncthreads();
-    // Wave w takes the row pairs (2w, 2w+1), (2w+16, 2w+17), ... of the
-    // segment: in zig-zag order each pair is one short and one long causal
-    // row, so the waves get equal work without a shared counter.
-    auto my_row = [&](int64_t j) -> int64_t { return (j >> 1) * (2 * kLdsWaves) + 2 * wave + (j & 1); };
-    if (sg.kind == kOrphan) {
-      for (int64_t j = 0; my_row(j) < n; ++j) {
-        const int64_t rel = r + my_row(j) - sg.rlo;
-        const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
-        if (g < a.Hkv && t < a.Tq)
-          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
-      }
-    } else if (sg.kind == kSeq && my_row(0) < n) {
-      int32_t lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(0), sg.lq_len));
-      Frag qn = load_q_frag(a, sg.qs + lq_n, sg.g);
-      for (int64_t j = 0; my_row(j) < n; ++j) {
-        const Frag qf = qn;
-        const int32_t lq = lq_n;
-        // Prefetch the next row's query (the current one again past the end,
-        // so every iteration issues the same loads).
-        const int64_t i2 = my_row(j + 1) < n ? my_row(j + 1) : my_row(j);
-        lq_n = static_cast<int32_t>(zigzag(sg.k0 + i2, sg.lq_len));
-        qn = load_q_frag(a, sg.qs + lq_n, sg.g);
-        lds_row<OutT, kOutQ>(a, kt, sg, sg.qs + lq, lq, qf);
-      }
-    }
-    r = sg.end;
-  }
 }
 
 // ------------------------------------------------------ K-streaming path
@@ -1187,6 +948,465 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
                     static_cast<int32_t>(done / 4), lq[k] >> 6, nch > 0 ? carry_out[k] : -INFINITY);
         }
       }
+    }
+    r = sg.end;
+  }
+}
+
+// --------------------------------------------- LDS-resident K, pipelined rows
+// For sequences with at most kLdsTiles*16 = 512 compressed keys (the "32K"
+// prefill shapes).  One persistent workgroup of eight waves per CU keeps the
+// whole compressed K of a (sequence, group) in LDS -- 128 KiB in MFMA
+// B-fragment order, filled by buffer-to-LDS loads -- and each wave computes
+// whole (token, group) rows; the next row's queries are loaded into a 4 KiB
+// per-wave LDS slot while the current row computes.
+//
+// Softmax with one exp per score: the exponentials are taken against the
+// exact max of the row's first 64-key quad (a reference, not the row max) and
+// kept in registers as f16 (rounded toward zero) until the row is done.  The
+// per-head sums and the final head sum both run on the matrix core: every
+// half-quad's f16 pack is multiplied by a 0/1 head selector into a per-head
+// accumulator, and at the end by the heads' 1/sum weights into the output.
+// Every exponential is positive, so a head's sum bounds each of its values:
+// one check per row -- every head's sum at most 2^14 -- proves that no f16
+// value overflowed and that every weight is a normal f16.  A row that fails
+// it (a later key far above the first quad's max) is redone against its
+// exact max, where the sums lie in [1, 512].
+//
+// Work split: the (group, token) rows of the batch are ordered by sequence,
+// then group, then token in zig-zag order (0, L-1, 1, L-2, ...), and each
+// workgroup takes one contiguous range of that order.  A range therefore
+// touches one or two (sequence, group) K blocks -- loaded once -- and its
+// causal work is balanced; wave w takes the row pairs (2w, 2w+1), (2w+16,
+// 2w+17), ... of a segment, each pair one short and one long row.
+constexpr int kRowSumLimit = 16384;  // 2^14: 1/sum is a normal f16
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Queries of token t (group g) -> the wave's LDS slot, fragment cc at
+// slot[cc * 64 + lane]; no registers are held while the loads fly.
+__device__ __forceinline__ void row_q_issue(const Stage1Args& a, bf16x8* slot, int64_t t, int g) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const __bf16* p = a.q + t * a.q_st + static_cast<int64_t>(g * kG + (lane & 15)) * a.q_sh +
+                    8 * (lane >> 4);
+#pragma unroll
+  for (int cc = 0; cc < kD / 32; ++cc)
+    __builtin_amdgcn_global_load_lds(p + 32 * cc, (lds_void_ptr)(slot + cc * kWave), 16, 0, 0);
+}
+
+// The slot's queries -> registers (waits for the wave's outstanding loads).
+__device__ __forceinline__ Frag row_q_read(const bf16x8* slot) {
+  const int lane = threadIdx.x & (kWave - 1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  Frag f;
+#pragma unroll
+  for (int cc = 0; cc < kD / 32; ++cc) f.v[cc] = slot[cc * kWave + lane];
+  return f;
+}
+
+// K block of (sequence, group) -> LDS in fragment order (tiles [0, ntl)):
+// unit ((jt*4 + cc)*64 + l) = k[ks + 16*jt + l%16][g][32*cc + 8*(l/16) .. +8].
+// Keys past the sequence (or past k) read as zero through the buffer range.
+template <int kWaves>
+__device__ __forceinline__ void row_k_issue(const Stage1Args& a, bf16x8* kt, const Segment& sg,
+                                            int ntl, int wave) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t keys_ok = sg.lk < a.Tk - sg.ks ? sg.lk : a.Tk - sg.ks;
+  keys_ok = keys_ok < 16 * ntl ? keys_ok : 16 * ntl;
+  if (sg.ks < 0) keys_ok = 0;
+  const __bf16* kb = a.k + (keys_ok > 0 ? static_cast<int64_t>(sg.ks) * a.k_st : 0) +
+                     static_cast<int64_t>(sg.g) * a.k_sh;
+  const uint32_t bytes = keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc(kb, bytes);
+  for (int f = wave; f < 4 * ntl; f += kWaves) {
+    const int jt = f >> 2, cc = f & 3;
+    const int key = 16 * jt + (lane & 15);
+    const int off = static_cast<int>((static_cast<int64_t>(key) * a.k_st + 32 * cc + 8 * (lane >> 4)) * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_ptr)(kt + f * kWave), 16, off, 0, 0, 0);
+  }
+}
+
+typedef __attribute__((address_space(3))) const bf16x8 lds_bf16x8;
+
+// The LDS key block as seen by one lane: fragment f at lo[f*64] for f < 64
+// and at hi[(f-64)*64] above, so every fragment's address is a base register
+// plus an immediate below 64 KiB (the ds_read offset field).  hi is opaque
+// to the compiler, which would otherwise keep one address register per
+// fragment of the upper half.
+struct KView {
+  lds_bf16x8* lo;
+  lds_bf16x8* hi;
+};
+
+__device__ __forceinline__ KView make_kview(const bf16x8* kt) {
+  const int lane = threadIdx.x & (kWave - 1);
+  KView v;
+  v.lo = (lds_bf16x8*)(kt) + lane;  // generic -> LDS address space
+  v.hi = v.lo + 64 * kWave;
+  asm volatile("" : "+v"(v.hi));
+  return v;
+}
+
+// Raw scores of half j (quad j/2, tiles 2(j%2) and 2(j%2)+1) of one row: the
+// half's eight K fragments are read from LDS at once (they return in order,
+// so each MFMA waits only for its own), then two interleaved accumulation
+// chains over the four K = 32 steps.
+__device__ __forceinline__ void row_half_mfma(KView kv, int j, const Frag& qf, f32x4 (&acc)[2]) {
+  const int f0 = (j >> 1) * 16 + (j & 1) * 8;  // first fragment of the half
+  lds_bf16x8* kq = f0 < 64 ? kv.lo + f0 * kWave : kv.hi + (f0 - 64) * kWave;  // (u, cc) at kq[(4u+cc)*64]
+  bf16x8 kf[kD / 32][2];
+#pragma unroll
+  for (int cc = 0; cc < kD / 32; ++cc)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) kf[cc][u] = kq[(4 * u + cc) * kWave];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int cc = 0; cc < kD / 32; ++cc)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf.v[cc], kf[cc][u], acc[u], 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pk_f16(float x, float y) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
+}
+
+// Per-head max of a quad's raw scores (kMasked: over keys < vis), into m.
+template <bool kMasked>
+__device__ __forceinline__ void row_quad_max(const f32x4 (&sa)[2], const f32x4 (&sb)[2], int key0,
+                                             int32_t vis, float (&m)[4]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const f32x4& s = t < 2 ? sa[t] : sb[t - 2];
+    // key0 + 16t + lane%16 < vis, as a lane index against a scalar limit
+    const bool ok = !kMasked || (lane & 15) < __builtin_amdgcn_readfirstlane(vis - key0 - 16 * t);
+    m[0] = fmaxf(m[0], ok ? s.x : -INFINITY);
+    m[1] = fmaxf(m[1], ok ? s.y : -INFINITY);
+    m[2] = fmaxf(m[2], ok ? s.z : -INFINITY);
+    m[3] = fmaxf(m[3], ok ? s.w : -INFINITY);
+  }
+}
+
+// Exponentials p = exp2(c*s + mc) of half j (zeroed for keys >= vis when
+// kMasked) -> pw[j/2][j%2] as the f16 pack in the B layout of the head-sum
+// MFMA (tile 0's four heads, then tile 1's), and their per-head sums into
+// lsum: with A = `sel` (row m has ones at the k-slots of head m in both
+// tiles), D[head][n] adds the head's two values of key column n.  Summed over
+// the row, lane group g holds heads 4g..4g+3 per key column; a 16-lane sum
+// finishes the per-head sums.
+template <bool kMasked, int kOutQ>
+__device__ __forceinline__ void row_stage_exp(int j, const f32x4 (&s)[2], float c,
+                                              const float (&mc)[4], int32_t vis, f16x8 sel,
+                                              f16x8 (&pw)[kOutQ][2], f32x4& lsum) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t pk[4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].x, c, mc[0]));
+    float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].y, c, mc[1]));
+    float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].z, c, mc[2]));
+    float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].w, c, mc[3]));
+    if constexpr (kMasked) {
+      const bool ok = (lane & 15) < __builtin_amdgcn_readfirstlane(vis - 32 * j - 16 * u);
+      p0 = ok ? p0 : 0.f;
+      p1 = ok ? p1 : 0.f;
+      p2 = ok ? p2 : 0.f;
+      p3 = ok ? p3 : 0.f;
+    }
+    pk[2 * u] = pk_f16(p0, p1);
+    pk[2 * u + 1] = pk_f16(p2, p3);
+  }
+  const f16x8 v = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+  pw[j >> 1][j & 1] = v;
+  lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, v, lsum, 0, 0, 0);
+}
+
+// The exponentials of a row's visible halves (half j = keys 32j..32j+31) into
+// pw, their per-head sums into lsum.  Software pipeline over halves: stage j
+// issues the score MFMAs of half j and exponentiates half j-1 in one basic
+// block, so the matrix core and the VALU work side by side; halves 0 and 1
+// (quad 0) are exponentiated together at stage 2, after (first) the
+// reference max mc is taken from quad 0 -- otherwise mc is given.  Only the
+// quad holding the causal limit is masked.  Accumulators alternate between
+// two register sets (quad 0 has its own).
+template <int kOutQ>
+__device__ __forceinline__ void row_pipeline(KView kl, const Frag& qf, int32_t vis, int nq,
+                                             bool first, float c, float (&mc)[4], f16x8 sel,
+                                             f16x8 (&pw)[kOutQ][2], f32x4& lsum) {
+  const int nq_full = vis >> 6;  // quads with every key visible
+  lsum = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 q0a[2], q0b[2], buf[2][2];
+  row_half_mfma(kl, 0, qf, q0a);
+  row_half_mfma(kl, 1, qf, q0b);
+  const bool m0 = nq_full < 1;  // quad 0 masked (wave-uniform)
+  if (first) {
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    if (m0)
+      row_quad_max<true>(q0a, q0b, 0, vis, m);
+    else
+      row_quad_max<false>(q0a, q0b, 0, vis, m);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mc[r] = -c * grp_max16(m[r]);
+  }
+  // stage 2: half 2 (quad 1) with the exponentials of quad 0
+  if (nq > 1) {
+    row_half_mfma(kl, 2, qf, buf[0]);
+    row_stage_exp<false, kOutQ>(0, q0a, c, mc, vis, sel, pw, lsum);
+    row_stage_exp<false, kOutQ>(1, q0b, c, mc, vis, sel, pw, lsum);
+  } else {
+    row_stage_exp<true, kOutQ>(0, q0a, c, mc, vis, sel, pw, lsum);
+    row_stage_exp<true, kOutQ>(1, q0b, c, mc, vis, sel, pw, lsum);
+  }
+  // stage j >= 3: half j's MFMAs with half j-1's exponentials; the stage
+  // after the last half exponentiates it alone (masked: the row ends there).
+#pragma unroll
+  for (int j = 3; j <= 2 * kOutQ; ++j) {
+    if (j < 2 * nq) {
+      row_half_mfma(kl, j, qf, buf[j & 1]);
+      if (j - 1 >= 2 * nq_full)
+        row_stage_exp<true, kOutQ>(j - 1, buf[(j - 1) & 1], c, mc, vis, sel, pw, lsum);
+      else
+        row_stage_exp<false, kOutQ>(j - 1, buf[(j - 1) & 1], c, mc, vis, sel, pw, lsum);
+    } else if (j == 2 * nq) {
+      row_stage_exp<true, kOutQ>(j - 1, buf[(j - 1) & 1], c, mc, vis, sel, pw, lsum);
+    }
+  }
+}
+
+// Normalise, sum over the 16 heads on the matrix core and store one row: for
+// tiles u of a quad, B = the tile's f16 exponentials (lane (key n, group g)
+// holds heads 4g..4g+3 -- the accumulator layout of the score MFMA is the B
+// layout with heads as the reduction index), A = 1/sum of those heads placed
+// on rows 4u..4u+3.  Two K = 32 MFMAs (tiles 0,1 then 2,3, accumulated)
+// leave every lane of group u holding the output of tile u for key l%16,
+// i.e. the quad's 64 outputs in lane order.  The row is written by exactly
+// kOutQ 64-column stores: quads [0, nq) computed, the rest zeros.
+template <typename OutT, int kOutQ, int N>
+__device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const f16x8 (&pw)[N][2],
+                                          int nq) {
+  const int lane = threadIdx.x & (kWave - 1);
+  f16x8 wa, wb;
+  {
+    float inv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv[r] = __builtin_amdgcn_rcpf(L[r]);
+    const int m = lane & 15;  // A row of this lane
+    const _Float16 h0 = static_cast<_Float16>(inv[0]), h1 = static_cast<_Float16>(inv[1]);
+    const _Float16 h2 = static_cast<_Float16>(inv[2]), h3 = static_cast<_Float16>(inv[3]);
+    const _Float16 z = static_cast<_Float16>(0.f);
+    const bool lo_a = m < 4, hi_a = m >= 4 && m < 8, lo_b = m >= 8 && m < 12, hi_b = m >= 12;
+    wa = f16x8{lo_a ? h0 : z, lo_a ? h1 : z, lo_a ? h2 : z, lo_a ? h3 : z,
+               hi_a ? h0 : z, hi_a ? h1 : z, hi_a ? h2 : z, hi_a ? h3 : z};
+    wb = f16x8{lo_b ? h0 : z, lo_b ? h1 : z, lo_b ? h2 : z, lo_b ? h3 : z,
+               hi_b ? h0 : z, hi_b ? h1 : z, hi_b ? h2 : z, hi_b ? h3 : z};
+  }
+#pragma unroll
+  for (int qd = 0; qd < kOutQ; ++qd) {
+    float o = 0.f;
+    if (qd < N && qd < nq) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, pw[qd < N ? qd : 0][0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, pw[qd < N ? qd : 0][1], acc, 0, 0, 0);
+      o = acc.x;
+    }
+    store_out<OutT>(orow + 64 * qd + lane, o);
+  }
+}
+
+// Per-head sums of a row from the accumulated selector MFMAs; false when one
+// exceeds 2^14 (the first-quad reference was too low for f16).
+__device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
+  const float lv[4] = {lsum.x, lsum.y, lsum.z, lsum.w};
+  bool bad = false;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    L[r] = grp_sum16(lv[r]);
+    bad = bad || !(L[r] <= static_cast<float>(kRowSumLimit));
+  }
+  return __builtin_amdgcn_ballot_w64(bad) == 0;
+}
+
+// A row of exactly NQ visible quads, as one straight-line block: the scores,
+// the reference max from quad 0, the exponentials and their per-head sums,
+// quad by quad (the compiler interleaves one quad's MFMAs with the previous
+// quad's exponentials); only the last quad is masked.  Returns false, having
+// stored nothing, when the row needs its exact max.
+template <typename OutT, int NQ, int kOutQ>
+__device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, float c, f16x8 sel,
+                                         OutT* orow, const bf16x8* slot, bool more, Frag& qn) {
+  f16x8 pw[NQ][2];
+  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
+  float mc[4];
+  {
+    f32x4 sa[2], sb[2];
+    row_half_mfma(kl, 0, qf, sa);
+    row_half_mfma(kl, 1, qf, sb);
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    row_quad_max<NQ == 1>(sa, sb, 0, vis, m);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mc[r] = -c * grp_max16(m[r]);
+    row_stage_exp<NQ == 1, NQ>(0, sa, c, mc, vis, sel, pw, lsum);
+    row_stage_exp<NQ == 1, NQ>(1, sb, c, mc, vis, sel, pw, lsum);
+  }
+#pragma unroll
+  for (int qd = 1; qd < NQ; ++qd) {
+    f32x4 sa[2], sb[2];
+    row_half_mfma(kl, 2 * qd, qf, sa);
+    row_half_mfma(kl, 2 * qd + 1, qf, sb);
+    if (qd == NQ - 1) {
+      row_stage_exp<true, NQ>(2 * qd, sa, c, mc, vis, sel, pw, lsum);
+      row_stage_exp<true, NQ>(2 * qd + 1, sb, c, mc, vis, sel, pw, lsum);
+    } else {
+      row_stage_exp<false, NQ>(2 * qd, sa, c, mc, vis, sel, pw, lsum);
+      row_stage_exp<false, NQ>(2 * qd + 1, sb, c, mc, vis, sel, pw, lsum);
+    }
+  }
+  float L[4];
+  if (!row_sums(lsum, L)) return false;
+  if (more) qn = row_q_read(slot);
+  row_store<OutT, kOutQ, NQ>(orow, L, pw, NQ);
+  return true;
+}
+
+// One (token, group) row with the whole key block in LDS.  kOutQ = out_cols/64
+// is a compile-time count: the row is written by exactly kOutQ 64-column
+// stores (computed quads, then zeros).  A row of nq visible quads runs the
+// straight-line row_fast<nq>; a row whose first-quad reference fails runs
+// the general pipeline against its exact max.
+//
+// `slot` holds the next row's queries in flight when `more`: they are read
+// into qn after the scores and before this row's stores, whose completion the
+// read's wait would otherwise include.
+template <typename OutT, int kOutQ>
+__device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Segment& sg,
+                                        int32_t lq, const Frag& qf, f16x8 sel,
+                                        const bf16x8* slot, bool more, Frag& qn) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq;
+  OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
+  int32_t vis = sg.lk;
+  if (a.causal) {
+    vis = tdiv16(lq - 15) + sg.lk - tdiv16(sg.lq_len - 16 + 1);
+    vis = vis < 0 ? 0 : (vis > sg.lk ? sg.lk : vis);
+  }
+  vis = vis < 64 * kOutQ ? vis : 64 * kOutQ;  // keys past the output row are not written
+  vis = __builtin_amdgcn_readfirstlane(vis);   // wave-uniform: scalar branches below
+  const int nq = (vis + 63) >> 6;              // 64-key quads; 0 when nothing is visible
+  const float c = a.scale_log2;                // > 0 on this path
+  if (nq == 0) {
+    if (more) qn = row_q_read(slot);
+#pragma unroll
+    for (int qd = 0; qd < kOutQ; ++qd) store_out<OutT>(orow + 64 * qd + lane, 0.f);
+    return;
+  }
+  bool done = false;
+  switch (nq) {
+#define UNUM_ROW_CASE(N) \
+    case N: if constexpr (N <= kOutQ) done = row_fast<OutT, N, kOutQ>(kl, qf, vis, c, sel, orow, slot, more, qn); break;
+    UNUM_ROW_CASE(1) UNUM_ROW_CASE(2) UNUM_ROW_CASE(3) UNUM_ROW_CASE(4)
+    UNUM_ROW_CASE(5) UNUM_ROW_CASE(6) UNUM_ROW_CASE(7) UNUM_ROW_CASE(8)
+#undef UNUM_ROW_CASE
+    default: break;
+  }
+  if (done) return;
+  // Rare: the exact row max from a pass over the scores alone, then the
+  // exponentials against it (every per-head sum then lies in [1, 512]).
+  float mc[4];
+  {
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int qd = 0; qd < kOutQ; ++qd) {
+      if (qd < nq) {
+        f32x4 sa[2], sb[2];
+        row_half_mfma(kl, 2 * qd, qf, sa);
+        row_half_mfma(kl, 2 * qd + 1, qf, sb);
+        row_quad_max<true>(sa, sb, 64 * qd, vis, mx);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mc[r] = -c * grp_max16(mx[r]);
+  }
+  f16x8 pw[kOutQ][2];
+  f32x4 lsum;
+  row_pipeline<kOutQ>(kl, qf, vis, nq, false, c, mc, sel, pw, lsum);
+  float L[4];
+  row_sums(lsum, L);
+  if (more) qn = row_q_read(slot);
+  row_store<OutT, kOutQ, kOutQ>(orow, L, pw, nq);
+}
+
+template <typename OutT, int kOutQ>
+__global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
+  __shared__ bf16x8 kt[kLdsUnits];                             // 128 KiB
+  __shared__ bf16x8 qslot[kLdsWaves][(kD / 32) * kWave];       // 8 x 4 KiB
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & (kWave - 1);
+  bf16x8* slot = qslot[wave];
+  const KView kl = make_kview(kt);
+  // Per-head sum selector (A operand): row m has ones at the k-slots of head
+  // m in both tiles, i.e. lane (m, g) at j with 4g + j%4 == m.
+  f16x8 sel;
+  {
+    const int m = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      sel[jj] = static_cast<_Float16>(4 * g + (jj & 3) == m ? 1.f : 0.f);
+  }
+  const int64_t r_begin = n_rows * blockIdx.x / gridDim.x;
+  const int64_t r_end = n_rows * (blockIdx.x + 1) / gridDim.x;
+  for (int64_t r = r_begin; r < r_end;) {
+    const Segment sg = find_segment(a, r, r_end);
+    const int64_t n = sg.end - r;
+    __syncthreads();  // the previous segment is done with kt
+    // Wave w takes the row pairs (2w, 2w+1), (2w+16, 2w+17), ... of the
+    // segment: in zig-zag order each pair is one short and one long causal
+    // row, so the waves get equal work without a shared counter.
+    auto my_row = [&](int64_t j) -> int64_t { return (j >> 1) * (2 * kLdsWaves) + 2 * wave + (j & 1); };
+    if (sg.kind == kOrphan) {
+      for (int64_t j = 0; my_row(j) < n; ++j) {
+        const int64_t rel = r + my_row(j) - sg.rlo;
+        const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
+        if (g < a.Hkv && t < a.Tq)
+          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+      }
+      r = sg.end;
+      continue;
+    }
+    if (sg.kind != kSeq) {
+      r = sg.end;
+      continue;
+    }
+    if (sg.lk > 0) {
+      int ntl = 4 * ((sg.lk + 63) >> 6);
+      ntl = ntl < 4 * kOutQ ? ntl : 4 * kOutQ;
+      row_k_issue<kLdsWaves>(a, kt, sg, ntl, wave);
+    }
+    const bool any = my_row(0) < n;
+    int32_t lq_n = 0;
+    if (any) {
+      lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(0), sg.lq_len));
+      row_q_issue(a, slot, sg.qs + lq_n, sg.g);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // kt is filled
+    if (!any) {
+      r = sg.end;
+      continue;
+    }
+    Frag qn = row_q_read(slot);
+    for (int64_t j = 0; my_row(j) < n; ++j) {
+      const Frag qf = qn;
+      const int32_t lq = lq_n;
+      // Next row's queries -> the slot (its previous contents are in qf).
+      const bool more = my_row(j + 1) < n;
+      if (more) {
+        lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(j + 1), sg.lq_len));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        row_q_issue(a, slot, sg.qs + lq_n, sg.g);
+      }
+      lds_row<OutT, kOutQ>(a, kl, sg, lq, qf, sel, slot, more, qn);
     }
     r = sg.end;
   }
