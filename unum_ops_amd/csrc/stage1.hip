@@ -955,11 +955,15 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 
 // --------------------------------------------- LDS-resident K, pipelined rows
 // For sequences with at most kLdsTiles*16 = 512 compressed keys (the "32K"
-// prefill shapes).  One persistent workgroup of eight waves per CU keeps the
+// prefill shapes).  One persistent workgroup of twelve waves per CU keeps the
 // whole compressed K of a (sequence, group) in LDS -- 128 KiB in MFMA
 // B-fragment order, filled by buffer-to-LDS loads -- and each wave computes
-// whole (token, group) rows; the next row's queries are loaded into a 4 KiB
-// per-wave LDS slot while the current row computes.
+// whole (token, group) rows; the next row's queries load into registers
+// while the current row computes.  Every row reads 16 KiB of K fragments
+// from LDS per 64-key quad, and the LDS delivers more bytes per clock the
+// more waves issue reads: twelve waves (three per SIMD, at most 168 VGPRs)
+// measured faster than eight (which leave room for more registers) and than
+// sixteen (which spill).
 //
 // Softmax with one exp per score: the exponentials are taken against the
 // exact max of the row's first 64-key quad (a reference, not the row max) and
@@ -977,32 +981,12 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 // then group, then token in zig-zag order (0, L-1, 1, L-2, ...), and each
 // workgroup takes one contiguous range of that order.  A range therefore
 // touches one or two (sequence, group) K blocks -- loaded once -- and its
-// causal work is balanced; wave w takes the row pairs (2w, 2w+1), (2w+16,
-// 2w+17), ... of a segment, each pair one short and one long row.
+// causal work is balanced; wave w takes the row pairs (2w, 2w+1), (2w+24,
+// 2w+25), ... of a segment, each pair one short and one long row.
 constexpr int kRowSumLimit = 16384;  // 2^14: 1/sum is a normal f16
+constexpr int kRowWaves = 12;        // 768 threads: three waves per SIMD
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-// Queries of token t (group g) -> the wave's LDS slot, fragment cc at
-// slot[cc * 64 + lane]; no registers are held while the loads fly.
-__device__ __forceinline__ void row_q_issue(const Stage1Args& a, bf16x8* slot, int64_t t, int g) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const __bf16* p = a.q + t * a.q_st + static_cast<int64_t>(g * kG + (lane & 15)) * a.q_sh +
-                    8 * (lane >> 4);
-#pragma unroll
-  for (int cc = 0; cc < kD / 32; ++cc)
-    __builtin_amdgcn_global_load_lds(p + 32 * cc, (lds_void_ptr)(slot + cc * kWave), 16, 0, 0);
-}
-
-// The slot's queries -> registers (waits for the wave's outstanding loads).
-__device__ __forceinline__ Frag row_q_read(const bf16x8* slot) {
-  const int lane = threadIdx.x & (kWave - 1);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  Frag f;
-#pragma unroll
-  for (int cc = 0; cc < kD / 32; ++cc) f.v[cc] = slot[cc * kWave + lane];
-  return f;
-}
 
 // K block of (sequence, group) -> LDS in fragment order (tiles [0, ntl)):
 // unit ((jt*4 + cc)*64 + l) = k[ks + 16*jt + l%16][g][32*cc + 8*(l/16) .. +8].
@@ -1235,7 +1219,7 @@ __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
 // stored nothing, when the row needs its exact max.
 template <typename OutT, int NQ, int kOutQ>
 __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, float c, f16x8 sel,
-                                         OutT* orow, const bf16x8* slot, bool more, Frag& qn) {
+                                         OutT* orow) {
   f16x8 pw[NQ][2];
   f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
   float mc[4];
@@ -1265,7 +1249,6 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
   }
   float L[4];
   if (!row_sums(lsum, L)) return false;
-  if (more) qn = row_q_read(slot);
   row_store<OutT, kOutQ, NQ>(orow, L, pw, NQ);
   return true;
 }
@@ -1275,14 +1258,9 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
 // stores (computed quads, then zeros).  A row of nq visible quads runs the
 // straight-line row_fast<nq>; a row whose first-quad reference fails runs
 // the general pipeline against its exact max.
-//
-// `slot` holds the next row's queries in flight when `more`: they are read
-// into qn after the scores and before this row's stores, whose completion the
-// read's wait would otherwise include.
 template <typename OutT, int kOutQ>
 __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Segment& sg,
-                                        int32_t lq, const Frag& qf, f16x8 sel,
-                                        const bf16x8* slot, bool more, Frag& qn) {
+                                        int32_t lq, const Frag& qf, f16x8 sel) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq;
   OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
@@ -1296,7 +1274,6 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Seg
   const int nq = (vis + 63) >> 6;              // 64-key quads; 0 when nothing is visible
   const float c = a.scale_log2;                // > 0 on this path
   if (nq == 0) {
-    if (more) qn = row_q_read(slot);
 #pragma unroll
     for (int qd = 0; qd < kOutQ; ++qd) store_out<OutT>(orow + 64 * qd + lane, 0.f);
     return;
@@ -1304,7 +1281,7 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Seg
   bool done = false;
   switch (nq) {
 #define UNUM_ROW_CASE(N) \
-    case N: if constexpr (N <= kOutQ) done = row_fast<OutT, N, kOutQ>(kl, qf, vis, c, sel, orow, slot, more, qn); break;
+    case N: if constexpr (N <= kOutQ) done = row_fast<OutT, N, kOutQ>(kl, qf, vis, c, sel, orow); break;
     UNUM_ROW_CASE(1) UNUM_ROW_CASE(2) UNUM_ROW_CASE(3) UNUM_ROW_CASE(4)
     UNUM_ROW_CASE(5) UNUM_ROW_CASE(6) UNUM_ROW_CASE(7) UNUM_ROW_CASE(8)
 #undef UNUM_ROW_CASE
@@ -1333,17 +1310,14 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Seg
   row_pipeline<kOutQ>(kl, qf, vis, nq, false, c, mc, sel, pw, lsum);
   float L[4];
   row_sums(lsum, L);
-  if (more) qn = row_q_read(slot);
   row_store<OutT, kOutQ, kOutQ>(orow, L, pw, nq);
 }
 
 template <typename OutT, int kOutQ>
-__global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
+__global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
   __shared__ bf16x8 kt[kLdsUnits];                             // 128 KiB
-  __shared__ bf16x8 qslot[kLdsWaves][(kD / 32) * kWave];       // 8 x 4 KiB
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & (kWave - 1);
-  bf16x8* slot = qslot[wave];
   const KView kl = make_kview(kt);
   // Per-head sum selector (A operand): row m has ones at the k-slots of head
   // m in both tiles, i.e. lane (m, g) at j with 4g + j%4 == m.
@@ -1360,10 +1334,10 @@ __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args
     const Segment sg = find_segment(a, r, r_end);
     const int64_t n = sg.end - r;
     __syncthreads();  // the previous segment is done with kt
-    // Wave w takes the row pairs (2w, 2w+1), (2w+16, 2w+17), ... of the
+    // Wave w takes the row pairs (2w, 2w+1), (2w+24, 2w+25), ... of the
     // segment: in zig-zag order each pair is one short and one long causal
     // row, so the waves get equal work without a shared counter.
-    auto my_row = [&](int64_t j) -> int64_t { return (j >> 1) * (2 * kLdsWaves) + 2 * wave + (j & 1); };
+    auto my_row = [&](int64_t j) -> int64_t { return (j >> 1) * (2 * kRowWaves) + 2 * wave + (j & 1); };
     if (sg.kind == kOrphan) {
       for (int64_t j = 0; my_row(j) < n; ++j) {
         const int64_t rel = r + my_row(j) - sg.rlo;
@@ -1381,13 +1355,14 @@ __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args
     if (sg.lk > 0) {
       int ntl = 4 * ((sg.lk + 63) >> 6);
       ntl = ntl < 4 * kOutQ ? ntl : 4 * kOutQ;
-      row_k_issue<kLdsWaves>(a, kt, sg, ntl, wave);
+      row_k_issue<kRowWaves>(a, kt, sg, ntl, wave);
     }
     const bool any = my_row(0) < n;
     int32_t lq_n = 0;
+    Frag qn;
     if (any) {
       lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(0), sg.lq_len));
-      row_q_issue(a, slot, sg.qs + lq_n, sg.g);
+      qn = load_q_frag(a, sg.qs + lq_n, sg.g);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // kt is filled
@@ -1395,18 +1370,15 @@ __global__ __launch_bounds__(kLdsWaves* kWave) void stage1_lds_kernel(Stage1Args
       r = sg.end;
       continue;
     }
-    Frag qn = row_q_read(slot);
     for (int64_t j = 0; my_row(j) < n; ++j) {
       const Frag qf = qn;
       const int32_t lq = lq_n;
-      // Next row's queries -> the slot (its previous contents are in qf).
-      const bool more = my_row(j + 1) < n;
-      if (more) {
+      // The next row's queries load into registers while this row computes.
+      if (my_row(j + 1) < n) {
         lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(j + 1), sg.lq_len));
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        row_q_issue(a, slot, sg.qs + lq_n, sg.g);
+        qn = load_q_frag(a, sg.qs + lq_n, sg.g);
       }
-      lds_row<OutT, kOutQ>(a, kl, sg, lq, qf, sel, slot, more, qn);
+      lds_row<OutT, kOutQ>(a, kl, sg, lq, qf, sel);
     }
     r = sg.end;
   }
@@ -1460,10 +1432,10 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, hipStream_t s) {
     hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, true>),
                        dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp, n_rows);
   } else if (path == kPathLds) {
-    int64_t grid = (n_rows + kLdsWaves - 1) / kLdsWaves;
+    int64_t grid = (n_rows + kRowWaves - 1) / kRowWaves;
     const int64_t cus = num_cus();
     grid = grid < cus ? grid : cus;
-    const dim3 g(static_cast<unsigned>(grid)), b(kLdsWaves * kWave);
+    const dim3 g(static_cast<unsigned>(grid)), b(kRowWaves * kWave);
     switch (a.out_cols / 64) {
 #define UNUM_LDS_CASE(N) \
       case N: hipLaunchKernelGGL((stage1_lds_kernel<OutT, N>), g, b, 0, s, a, n_rows); break;
