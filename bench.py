@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
                                        "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
                                        "compress_keys_cfg5", "stage1_maxpool",
-                                       "stage1_maxpool_cfg5", "copy"], default=None,
+                                       "stage1_maxpool_cfg5", "stage1_cfg4", "copy"],
+                    default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
@@ -88,8 +89,15 @@ def build_inputs(dev):
               cache=torch.zeros(1, dtype=torch.int32, device=dev),
               cu_q_cpu=p5["cu_seqlens_q"], cu_k_cpu=p5["cu_seqlens_k"])
     del pooled
+    # cfg4: 64 decode / chunked-prefill sequences (1-16 new tokens after
+    # 16K-64K cached ones), stage 1 over their compressed keys.
+    p4 = workloads.cfg4_pipeline()
+    c4 = dict(q=p4["q"].to(dev), k=p4["k"].to(dev), cu_q=p4["cu_seqlens_q"].to(dev),
+              cu_k=p4["cu_seqlens_k"].to(dev), max_seqlen_k=p4["max_seqlen_k"],
+              cu_q_cpu=p4["cu_seqlens_q"], cu_k_cpu=p4["cu_seqlens_k"])
+    c5["cfg4"] = c4
     torch.cuda.synchronize()
-    log(f"cfg5 inputs ready ({time.time() - t0:.1f}s)")
+    log(f"cfg4/cfg5 inputs ready ({time.time() - t0:.1f}s)")
     return s1, s1g, mp, mpg, bt, c5
 
 
@@ -164,6 +172,12 @@ def main():
                                             c5["max_context_len"],
                                             max_seqlen_k=c5["max_seqlen_k"], causal=True)
 
+    c4 = c5["cfg4"]
+
+    def op_stage1_cfg4():
+        return infllmv2_attn_stage1(c4["q"], c4["k"], None, c4["cu_q"], c4["cu_k"],
+                                    max_seqlen_k=c4["max_seqlen_k"], causal=True)
+
     def op_compress_cfg5():
         return compress_keys(c5["raw"], c5["cu_raw"], plan=plan5)
 
@@ -174,7 +188,7 @@ def main():
     extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5),
              ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5),
              ("compress_keys_cfg5", op_compress_cfg5), ("stage1_maxpool", op_stage1_maxpool),
-             ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5)]
+             ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5), ("stage1_cfg4", op_stage1_cfg4)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -248,6 +262,18 @@ def main():
                                     flop=flop, bytes=nbytes, bound="mfma",
                                     config="cfg5 4096-token chunk of a 135168-token context, "
                                            "Hq32/Hkv2/D128, fp32 out [2,4096,8448]")
+    if "stage1_cfg4" in per_op:
+        ncols = -(-c4["max_seqlen_k"] // 128) * 128
+        flop, nbytes, _ = workloads.stage1_work(c4["cu_q_cpu"], c4["cu_k_cpu"], 32, 2, 128, ncols)
+        t = per_op["stage1_cfg4"] * 1e-3
+        comps["stage1_cfg4"] = dict(us=per_op["stage1_cfg4"] * 1e3, tflops=flop / t / 1e12,
+                                    pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                                    gbs=nbytes / t / 1e9,
+                                    pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                    flop=flop, bytes=nbytes, bound="hbm",
+                                    config=f"cfg4 64 sequences, 1-16 new tokens after 16K-64K "
+                                           f"cached, Hq32/Hkv2/D128, fp32 out "
+                                           f"[2,{int(c4['cu_q_cpu'][-1])},{ncols}]")
     if "maxpool_cfg5" in per_op:
         nbytes = workloads.maxpool_bytes(c5["cu_q_cpu"], c5["cu_k_cpu"], [0], 2,
                                          -(-c5["max_context_len"] // 64))

@@ -71,8 +71,12 @@ int unum_abi_version(void);
  * keys of a sequence at j >= out_cols are not (the reference writes past the
  * row there).
  *
- * `workspace` must hold unum_infllmv2_attn_stage1_workspace_size(...) bytes
- * (it may be NULL when that size is 0).
+ * `workspace` (device memory, caller-owned, no initial contents needed) of
+ * unum_infllmv2_attn_stage1_workspace_size(...) bytes lets rows over 512 keys
+ * split their keys between workgroups (two launches on `stream`: per-split
+ * log-sum-exps, then the scores); NULL or a smaller workspace runs the
+ * whole-row kernel, with the same results to within fp32 rounding.  Calls that
+ * share one workspace must not overlap.
  */
 int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                               const void* k, int64_t k_stride_t, int64_t k_stride_h,
@@ -83,7 +87,9 @@ int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_strid
                               int32_t causal, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* Workspace bytes unum_infllmv2_attn_stage1 needs for this problem (>= 0). */
+/* Workspace bytes unum_infllmv2_attn_stage1 uses for this problem on the
+ * current device (>= 0; 0: the problem is not split), with out_cols =
+ * round_up(max_seqlen_k, 128). */
 int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t Hq,
                                                  int64_t Hkv, int64_t D,
                                                  int64_t max_seqlen_k);

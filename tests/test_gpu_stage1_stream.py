@@ -99,3 +99,49 @@ def test_large_magnitude_keys(dev):
     d = workloads.stage1_inputs([50, 16], [20000, 7000], seed=46)
     d["k"] = (d["k"].float() * 40.0).to(torch.bfloat16)
     _run_check(d, dev)
+
+
+def test_decode_mix_many_short_sequences(dev):
+    # cfg4's shape in small: many sequences of a few query tokens over long
+    # contexts -- the rows are split over keys between workgroups.
+    g = torch.Generator().manual_seed(47)
+    q_lens = torch.randint(1, 17, (12,), generator=g).tolist()
+    ctx = torch.randint(8000, 20000, (12,), generator=g).tolist()
+    d = workloads.stage1_inputs(q_lens, ctx, seed=47, raw_keys=False)
+    _run_check(d, dev)
+
+
+@pytest.mark.parametrize("q_lens,ctx", [([40, 9], [9000, 30000]), ([300], [12000])])
+def test_workspace_absent_runs_the_unsplit_kernel(q_lens, ctx, dev):
+    """The C entry point without a workspace runs the whole-row kernel; with one
+    it splits the keys.  Both match the oracle."""
+    import ctypes
+
+    from unum_ops_amd import _lib
+
+    d = workloads.stage1_inputs(q_lens, ctx, seed=48, raw_keys=False)
+    exp = oracle_stage1(d["q"], d["k"], None, d["cu_seqlens_q"], d["cu_seqlens_k"],
+                        max_seqlen_k=d["max_seqlen_k"], causal=True)
+    q, k = d["q"].to(dev), d["k"].to(dev)
+    cu_q, cu_k = d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev)
+    B = cu_q.numel() - 1
+    cols = exp.shape[-1]
+    lib = _lib.load()
+    ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(B, q.shape[0], 32, 2, 128,
+                                                            d["max_seqlen_k"])
+    assert ws_bytes > 0
+    outs = []
+    for with_ws in (False, True):
+        out = torch.full((2, q.shape[0], cols), float("nan"), device=dev)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if with_ws else None
+        st = lib.unum_infllmv2_attn_stage1(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+            _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(out), _lib.UNUM_DTYPE_F32,
+            B, q.shape[0], k.shape[0], 32, 2, 128, d["max_seqlen_k"], cols,
+            ctypes.c_float(128 ** -0.5), 1, _lib.ptr(ws), ws_bytes if with_ws else 0,
+            _lib.stream_ptr(dev))
+        _lib.check(st, "stage1")
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu(), exp, atol=ATOL, rtol=RTOL)
+        outs.append(out)
+    torch.testing.assert_close(outs[0], outs[1], atol=1e-4, rtol=1e-3)

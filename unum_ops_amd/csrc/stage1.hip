@@ -671,9 +671,23 @@ __device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const F
   }
 }
 
-template <typename OutT, int W, int TW, bool kPool>
+// Key splits (kSplit != 0): for rows with few tokens and many keys (decode
+// against a long cache) one workgroup per 16-row piece leaves most of the
+// GPU idle, so the keys are split too.  kSplit == 1 runs the first pass over
+// one split (blockIdx.y) and writes each (row, head)'s log2-sum-exp of the
+// split, c*max + log2(sum), to `ws`; kSplit == 2 combines a row's splits into
+// the bias and runs the second pass over its split, writing that split's
+// columns.  The two launches are the reference's two passes.
+struct Stage1Split {
+  float* ws;        // [pieces][n_splits][16 rows][16 heads]
+  int32_t chunks;   // 256-key chunks per split
+  int32_t n_splits;
+};
+
+template <typename OutT, int W, int TW, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
-                                                                 int64_t n_rows) {
+                                                                 Stage1Split sp, int64_t n_rows) {
+  static_assert(!(kPool && kSplit), "the fused pool runs on whole rows");
   __shared__ bf16x8 kbuf[2][kStChunkUnits];
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
   // per-token rows and store descriptors in scalar registers.
@@ -698,11 +712,13 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   }
   const uint32_t row_bytes = static_cast<uint32_t>(a.out_cols * sizeof(OutT));
 
+  const int split = kSplit ? static_cast<int>(blockIdx.y) : 0;
+  constexpr int kChunkKeys = kStChunkTiles * 16;
   for (int64_t r = r_begin; r < r_end;) {
     const Segment sg = find_segment(a, r, r_end);
     const int64_t n = sg.end - r;
     if (sg.kind == kOrphan) {
-      for (int64_t j = wave; j < n; j += W) {
+      for (int64_t j = wave; j < n && kSplit != 1 && split == 0; j += W) {
         const int64_t rel = r + j - sg.rlo;
         const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
         if (g < a.Hkv && t < a.Tq) {
@@ -741,7 +757,16 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     // Causal visibility grows with the token, so the piece's last token sees
     // the most keys.
     const int32_t kv_hi = vis_of(static_cast<int32_t>(sg.k0 + n - 1));
-    const int nch = (kv_hi + kStChunkTiles * 16 - 1) / (kStChunkTiles * 16);
+    const int nch = (kv_hi + kChunkKeys - 1) / kChunkKeys;
+    // Chunks of this launch: all of them, or those of this key split.
+    const int ch_lo = kSplit ? (split * sp.chunks < nch ? split * sp.chunks : nch) : 0;
+    const int ch_hi = kSplit ? (ch_lo + sp.chunks < nch ? ch_lo + sp.chunks : nch) : nch;
+    // Workspace row of token k: the row it is computed for (a repeated
+    // token reads the row of the one it repeats).
+    auto ws_row = [&](int k) -> int64_t {
+      const int64_t i = own[k] ? wave + static_cast<int64_t>(W) * k : n - 1;
+      return ((static_cast<int64_t>(blockIdx.x) * sp.n_splits) * R + (r - r_begin) + i) * 16;
+    };
     Frag qf[TW];
 #pragma unroll
     for (int k = 0; k < TW; ++k) qf[k] = load_q_frag(a, sg.qs + lq[k], sg.g);
@@ -753,10 +778,38 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, k_bytes);
 
     float nb[TW][4];  // pass-2 bias: p = exp2(c*s + nb)
+    if constexpr (kSplit == 2) {
+      // Combine the splits' log2-sum-exps of each (row, head): lane group g
+      // reads heads 4g..4g+3 of the splits that hold visible keys.
+      const int64_t split_stride = static_cast<int64_t>(R) * 16;
+#pragma unroll
+      for (int k = 0; k < TW; ++k) {
+        const int ns = (vis[k] + sp.chunks * kChunkKeys - 1) / (sp.chunks * kChunkKeys);
+        const float* src = sp.ws + ws_row(k) + 4 * (lane >> 4);
+        float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < ns; ++t) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(src + t * split_stride);
+          const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const float nm = fmaxf(m[rr], vv[rr]);
+            if (nm != -INFINITY) {
+              sum[rr] = sum[rr] * __builtin_amdgcn_exp2f(m[rr] - nm) +
+                        __builtin_amdgcn_exp2f(vv[rr] - nm);
+              m[rr] = nm;
+            }
+          }
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          nb[k][rr] = sum[rr] > 0.f ? -(m[rr] + __builtin_amdgcn_logf(sum[rr])) : -INFINITY;
+      }
+    }
     [[maybe_unused]] float carry_out[TW];  // fused pool: each token's last tap so far
 #pragma unroll
     for (int k = 0; k < TW; ++k) carry_out[k] = -INFINITY;
-    for (int pass = 0; pass < 2 && nch > 0; ++pass) {
+    for (int pass = kSplit == 2 ? 1 : 0; pass < (kSplit == 1 ? 1 : 2) && ch_hi > ch_lo; ++pass) {
       float mref[TW][4], mc[TW][4], l[TW][4];
 #pragma unroll
       for (int k = 0; k < TW; ++k)
@@ -781,12 +834,12 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
       }
       u32x4 stage[kPer];
       __syncthreads();  // the previous user of kbuf is done
-      stream_issue<W>(kr, a.k_st, 0, stage);
+      stream_issue<W>(kr, a.k_st, ch_lo, stage);
       stream_commit<W>(kbuf[0], stage);
       __syncthreads();
-      for (int ch = 0; ch < nch; ++ch) {
-        const bf16x8* buf = kbuf[ch & 1];
-        if (ch + 1 < nch) stream_issue<W>(kr, a.k_st, ch + 1, stage);
+      for (int ch = ch_lo; ch < ch_hi; ++ch) {
+        const bf16x8* buf = kbuf[(ch - ch_lo) & 1];
+        if (ch + 1 < ch_hi) stream_issue<W>(kr, a.k_st, ch + 1, stage);
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           f32x4 acc[TW][4];
@@ -806,7 +859,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
                   acc[k][u].w = ok ? acc[k][u].w : -INFINITY;
                 }
             }
-            if (ch == 0 && qd == 0) {  // the reference: the first quad's exact max
+            if (ch == ch_lo && qd == 0) {  // the reference: the first quad's exact max
 #pragma unroll
               for (int k = 0; k < TW; ++k) {
                 float q4[4];
@@ -917,7 +970,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             }
           }
         }
-        if (ch + 1 < nch) stream_commit<W>(kbuf[(ch + 1) & 1], stage);
+        if (ch + 1 < ch_hi) stream_commit<W>(kbuf[(ch + 1 - ch_lo) & 1], stage);
         __syncthreads();
       }
       if (pass == 0) {
@@ -932,16 +985,41 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             const float L = grp_sum16(part);
             nb[k][rr] = L > 0.f ? -(M * c + __builtin_amdgcn_logf(L)) : -INFINITY;
           }
+        if constexpr (kSplit == 1) {
+          // This split's log2-sum-exp per (row, head): lane 16g + j (j < 4)
+          // writes head 4g + j.
+          const int j = lane & 15;
+#pragma unroll
+          for (int k = 0; k < TW; ++k) {
+            const float v = j == 0 ? nb[k][0] : j == 1 ? nb[k][1] : j == 2 ? nb[k][2] : nb[k][3];
+            if (own[k] && j < 4)  // nb = -inf: no visible key, log2-sum-exp -inf
+              sp.ws[ws_row(k) + static_cast<int64_t>(split) * R * 16 + 4 * (lane >> 4) + j] =
+                  v == -INFINITY ? -INFINITY : -v;
+          }
+        }
       }
     }
-    // Columns past the streamed chunks.
+    if constexpr (kSplit == 1) {
+      // Rows with no visible key in this split: the second pass reads only
+      // the splits below a row's visible count.
+      r = sg.end;
+      continue;
+    }
+    // Columns past the streamed chunks (of this split's columns).
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
       if (own[k]) {
         const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k];
-        const int64_t done = static_cast<int64_t>(nch) * kStChunkTiles * 16;
-        if (!kPool || pp.write_scores)
-          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + row * a.out_cols, done, a.out_cols);
+        int64_t done = static_cast<int64_t>(nch) * kChunkKeys;
+        int64_t end = a.out_cols;
+        if constexpr (kSplit == 2) {
+          const int64_t s0 = static_cast<int64_t>(split) * sp.chunks * kChunkKeys;
+          const int64_t s1 = s0 + static_cast<int64_t>(sp.chunks) * kChunkKeys;
+          done = done > s0 ? done : s0;
+          end = s1 < end ? s1 : end;
+        }
+        if ((!kPool || pp.write_scores) && done < end)
+          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + row * a.out_cols, done, end);
         if constexpr (kPool) {
           // The last streamed column's tap is carried only when a chunk ran.
           pool_tail(pp, make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)),
@@ -1414,8 +1492,36 @@ Stage1Path stage1_path(const Stage1Args& a) {
   return mfma ? kPathRowMfma : kPathGeneric;
 }
 
+// Key-split plan of the streaming path: pieces of 16 rows times splits of
+// `chunks` 256-key chunks, about four workgroups per CU in all (one runs per
+// CU at a time; fewer left CUs idle on decode batches, more gave splits of
+// one chunk, whose load is never overlapped); the workspace holds one float
+// per (piece, split, row, head).
+struct SplitPlan {
+  int64_t pieces;
+  int32_t chunks, n_splits;
+  int64_t bytes;
+};
+
+SplitPlan split_plan(int64_t n_rows, int64_t out_cols) {
+  constexpr int64_t R = kStWaves * kStTokensPerWave;
+  constexpr int64_t kChunkKeys = kStChunkTiles * 16;
+  SplitPlan p{};
+  p.pieces = (n_rows + R - 1) / R;
+  const int64_t out_chunks = (out_cols + kChunkKeys - 1) / kChunkKeys;
+  const int64_t target = 4 * static_cast<int64_t>(num_cus());
+  int64_t chunks = (out_chunks * p.pieces + target - 1) / target;
+  chunks = chunks < 1 ? 1 : chunks;
+  const int64_t n_splits = out_chunks > 0 ? (out_chunks + chunks - 1) / chunks : 0;
+  p.chunks = static_cast<int32_t>(chunks);
+  p.n_splits = static_cast<int32_t>(n_splits < 65535 ? n_splits : 0);
+  p.bytes = p.n_splits >= 2 ? p.pieces * p.n_splits * R * 16 * static_cast<int64_t>(sizeof(float)) : 0;
+  return p;
+}
+
 template <typename OutT, bool kPool>
-int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, hipStream_t s) {
+int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t ws_bytes,
+                  hipStream_t s) {
   const Stage1Path path = stage1_path<OutT>(a);
   // The pool is fused into the K-streaming kernel only: in the LDS-resident
   // kernel (rows of at most 512 keys) the extra state pushed the row's
@@ -1429,8 +1535,9 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, hipStream_t s) {
   if constexpr (kPool) {
     constexpr int kTW = kStTokensPerWave;
     const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
-    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, true>),
-                       dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp, n_rows);
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, true, 0>),
+                       dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp,
+                       Stage1Split{}, n_rows);
   } else if (path == kPathLds) {
     int64_t grid = (n_rows + kRowWaves - 1) / kRowWaves;
     const int64_t cus = num_cus();
@@ -1446,9 +1553,22 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, hipStream_t s) {
     }
   } else if (path == kPathStream) {
     constexpr int kTW = kStTokensPerWave;
-    const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
-    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false>),
-                       dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp, n_rows);
+    const SplitPlan plan = split_plan(n_rows, a.out_cols);
+    const dim3 block(kStWaves * kWave);
+    if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes) {
+      const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
+      const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false, 1>), grid, block, 0, s,
+                         a, pp, sp, n_rows);
+      const int st = check_launch("infllmv2_attn_stage1");
+      if (st != UNUM_OK) return st;
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false, 2>), grid, block, 0, s,
+                         a, pp, sp, n_rows);
+    } else {
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false, 0>),
+                         dim3(static_cast<unsigned>(plan.pieces)), block, 0, s, a, pp,
+                         Stage1Split{}, n_rows);
+    }
   } else if (path == kPathRowMfma) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
     hipLaunchKernelGGL(stage1_mfma_kernel<OutT>, grid, dim3(256), 0, s, a);
@@ -1465,9 +1585,16 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, hipStream_t s) {
 }  // namespace
 }  // namespace unum
 
-extern "C" int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t, int64_t, int64_t,
-                                                            int64_t, int64_t, int64_t) {
-  return 0;
+extern "C" int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t Hq,
+                                                            int64_t Hkv, int64_t D,
+                                                            int64_t max_seqlen_k) {
+  using namespace unum;
+  (void)B;
+  // Only the streaming path (G = 16, D = 128, rows over 512 keys) splits keys.
+  if (Tq <= 0 || Hkv <= 0 || Hq != kG * Hkv || D != kD || max_seqlen_k <= 0) return 0;
+  const int64_t out_cols = (max_seqlen_k + 127) / 128 * 128;
+  if (out_cols <= kLdsTiles * 16) return 0;
+  return split_plan(Hkv * Tq, out_cols).bytes;
 }
 
 namespace unum {
@@ -1527,8 +1654,6 @@ extern "C" int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int6
                                          int32_t causal, void* workspace,
                                          int64_t workspace_bytes, void* stream) {
   using namespace unum;
-  (void)workspace;
-  (void)workspace_bytes;
   clear_error();
   Stage1Args a;
   const int st = stage1_args(a, q, q_stride_t, q_stride_h, k, k_stride_t, k_stride_h,
@@ -1538,8 +1663,10 @@ extern "C" int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int6
   UNUM_REQUIRE(out, "infllmv2_attn_stage1: null output");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (out_dtype) {
-    case UNUM_DTYPE_F32: return launch_stage1<float, false>(a, Stage1Pool{}, s);
-    case UNUM_DTYPE_BF16: return launch_stage1<uint16_t, false>(a, Stage1Pool{}, s);
+    case UNUM_DTYPE_F32:
+      return launch_stage1<float, false>(a, Stage1Pool{}, workspace, workspace_bytes, s);
+    case UNUM_DTYPE_BF16:
+      return launch_stage1<uint16_t, false>(a, Stage1Pool{}, workspace, workspace_bytes, s);
     default:
       UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "infllmv2_attn_stage1: unsupported out dtype %d", out_dtype);
   }
@@ -1571,5 +1698,5 @@ extern "C" int unum_infllmv2_attn_stage1_maxpool(
   pp.init_blocks = init_blocks;
   pp.local_blocks = local_blocks;
   pp.write_scores = scores != nullptr;
-  return launch_stage1<float, true>(a, pp, static_cast<hipStream_t>(stream));
+  return launch_stage1<float, true>(a, pp, nullptr, 0, static_cast<hipStream_t>(stream));
 }

@@ -87,10 +87,12 @@ def infllmv2_attn_stage1(q, k, v, cu_seqlens_q, cu_seqlens_k, cu_seqlens_v=None,
     if total_k == 0:
         return out.zero_()
     lib = _lib.load()
-    ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(
-        batch, total_q, n_heads, n_kv_heads, head_dim, max_seqlen_k)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     with torch.cuda.device(dev):
+        # Rows over 512 keys split their keys between workgroups through a
+        # small workspace (about 1 KiB per 16 rows and split).
+        ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(
+            batch, total_q, n_heads, n_kv_heads, head_dim, max_seqlen_k)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
         st = lib.unum_infllmv2_attn_stage1(
             _lib.ptr(q), q.stride(0), q.stride(1),
             _lib.ptr(k), k.stride(0), k.stride(1),
