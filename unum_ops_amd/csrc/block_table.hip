@@ -11,7 +11,8 @@
 // runs (1 KiB, one dwordx4 per lane).  The block-table gather for those
 // entries is one dwordx4 load when the four positions are in range and
 // 16-byte aligned, all four steps' loads issued before the first store.  The
-// kernel is bound by the output write.
+// kernel is bound by the output write; its stores are non-temporal (nothing
+// here re-reads the output).
 #include "common.h"
 
 namespace unum {
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a, int6
 #pragma unroll
     for (int st = 0; st < kIdsPerUnit / 4; ++st) {
       const int32_t k = kb + 4 * st + sub;
-      if (k < a.K) out[static_cast<int64_t>(k) * 16 + (lane & 15)] = i32x4{0, 0, 0, 0};
+      if (k < a.K) __builtin_nontemporal_store(i32x4{0, 0, 0, 0}, out + static_cast<int64_t>(k) * 16 + (lane & 15));
     }
     return;
   }
@@ -120,8 +121,8 @@ __global__ __launch_bounds__(256) void block_table_kernel(BlockTableArgs a, int6
     const int32_t k = kb + 4 * st + sub;
     const bool raw_ok = kVecTable && p0[st] >= 0 && p0[st] <= vec_hi;
     if (k < a.K)
-      out[static_cast<int64_t>(k) * 16 + (lane & 15)] =
-          finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h);
+      __builtin_nontemporal_store(finish4(a, row, raw[st], raw_ok, p0[st], limit_len, limit_pos, h),
+                                  out + static_cast<int64_t>(k) * 16 + (lane & 15));
   }
 }
 
