@@ -1,8 +1,8 @@
 """GPU parity of the K-streaming stage-1 kernel (rows longer than 512 compressed
 keys) against the fp32 oracle, at atol 1e-3 / rtol 1e-2.
 
-Cases aimed at the kernel's own structure: 16-token pieces that straddle
-sequence boundaries, tokens that see no key, chunks cut by the sequence end,
+Cases aimed at the kernel's own structure: pieces of tokens (16 on whole
+rows, 8 on key splits) that straddle sequence boundaries, tokens that see no key, chunks cut by the sequence end,
 tokens outside every sequence, bf16 output, strided queries, and scores that
 grow along the keys far enough to force the running reference maximum to
 move (the rare re-do path).
@@ -53,7 +53,7 @@ def test_tokens_without_visible_keys(dev):
 
 @pytest.mark.parametrize("ctx", [32 + 16 * 512, 32 + 16 * 513, 32 + 16 * 766])
 def test_chunk_boundaries(ctx, dev):
-    # compressed lengths 513 / 514 / 767: the last 256-key chunk is cut
+    # compressed lengths 513 / 514 / 767: the last 128-key chunk is cut
     d = workloads.stage1_inputs([20], [ctx], seed=ctx)
     _run_check(d, dev)
 

@@ -583,13 +583,16 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
 
 // ------------------------------------------------------ K-streaming path
 // For rows longer than the LDS-resident path holds (Kp > 512: long contexts,
-// decode against a large cache).  A workgroup of eight waves owns a piece of
-// up to 8*TW consecutive tokens of one (sequence, group); wave w computes the
-// tokens w, w+8, ... (TW of them), so every K fragment read from LDS feeds TW
-// score MFMAs.  K streams through two 64 KiB LDS buffers in the fragment order
-// of the resident path, 256 keys at a time: the next chunk's loads are issued
+// decode against a large cache).  A workgroup of W waves owns a piece of up
+// to W*TW consecutive tokens of one (sequence, group); wave w computes the
+// tokens w, w+W, ... (TW of them), so every K fragment read from LDS feeds TW
+// score MFMAs.  K streams through two LDS buffers in the fragment order of
+// the resident path, CT*16 keys at a time: the next chunk's loads are issued
 // into registers before the current chunk is computed and written to the free
-// buffer after it, with one barrier per chunk.
+// buffer after it, with one barrier per chunk.  Whole rows run eight waves;
+// key splits (below) run four, with half the LDS, so that two workgroups
+// share a CU and one's loads overlap the other's compute (measured 40%
+// faster on decode batches; eight waves measured faster on long chunks).
 //
 // The reference's two passes, with the VALU work per score kept to an fma, an
 // exp and one more op:
@@ -604,40 +607,34 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
 // Every quad of a streamed chunk is computed (keys past the visible range are
 // masked to 0), and stores past the row are dropped by the buffer range check,
 // so each chunk issues the same memory operations and waits stay exact.
-constexpr int kStChunkTiles = 16;                          // 256 keys
-constexpr int kStChunkUnits = kStChunkTiles * 4 * kWave;   // 4096 bf16x8 units: 64 KiB
-constexpr float kStLimit = 18446744073709551616.f;         // 2^64
-#ifndef UNUM_STREAM_TW
-#define UNUM_STREAM_TW 2
-#endif
-#ifndef UNUM_STREAM_WAVES
-#define UNUM_STREAM_WAVES 8
-#endif
-constexpr int kStTokensPerWave = UNUM_STREAM_TW;  // tokens sharing each K fragment
-constexpr int kStWaves = UNUM_STREAM_WAVES;       // waves per workgroup
+constexpr int kStChunkTiles = 8;           // 16-key tiles per streamed chunk (128 keys)
+constexpr float kStLimit = 18446744073709551616.f;  // 2^64
+constexpr int kStTokensPerWave = 2;  // tokens sharing each K fragment
+constexpr int kStWaves = 8;          // waves per workgroup on whole rows
+constexpr int kStSplitWaves = 4;     // waves per workgroup on key splits
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Issue the loads of chunk `ch` (keys 256*ch ..) of the piece's K block; keys
-// past the valid range read as zero (buffer range check).
-template <int W>
+// Issue the loads of chunk `ch` (keys CT*16*ch ..) of the piece's K block;
+// keys past the valid range read as zero (buffer range check).
+template <int W, int CT>
 __device__ __forceinline__ void stream_issue(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int ch,
-                                             u32x4 (&v)[kStChunkUnits / (W * kWave)]) {
+                                             u32x4 (&v)[CT * 4 / W]) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
 #pragma unroll
-  for (int i = 0; i < kStChunkUnits / (W * kWave); ++i) {
+  for (int i = 0; i < CT * 4 / W; ++i) {
     const int u = tid + i * W * kWave;
     const int jt = u >> 8, cc = (u >> 6) & 3, l = u & 63;
-    const int key = kStChunkTiles * 16 * ch + 16 * jt + (l & 15);
+    const int key = CT * 16 * ch + 16 * jt + (l & 15);
     const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (l >> 4)) * 2);
     v[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
   }
 }
-template <int W>
-__device__ __forceinline__ void stream_commit(bf16x8* buf, const u32x4 (&v)[kStChunkUnits / (W * kWave)]) {
+template <int W, int CT>
+__device__ __forceinline__ void stream_commit(bf16x8* buf, const u32x4 (&v)[CT * 4 / W]) {
 #pragma unroll
-  for (int i = 0; i < kStChunkUnits / (W * kWave); ++i) {
+  for (int i = 0; i < CT * 4 / W; ++i) {
     const int u = static_cast<int>(threadIdx.x) + i * W * kWave;
     buf[u] = __builtin_bit_cast(bf16x8, v[i]);
   }
@@ -689,18 +686,19 @@ struct Stage1Split {
   int32_t n_splits;
 };
 
-template <typename OutT, int W, int TW, bool kPool, int kSplit>
+template <typename OutT, int W, int TW, int CT, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
                                                                  Stage1Split sp, int64_t n_rows) {
   static_assert(!(kPool && kSplit), "the fused pool runs on whole rows");
-  __shared__ bf16x8 kbuf[2][kStChunkUnits];
+  static_assert((CT * 4) % W == 0, "every thread loads the same number of K units");
+  __shared__ bf16x8 kbuf[2][CT * 4 * kWave];
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
   // per-token rows and store descriptors in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & (kWave - 1);
   const float c = a.scale_log2;  // > 0 on this path
   constexpr int R = W * TW;
-  constexpr int kPer = kStChunkUnits / (W * kWave);
+  constexpr int kPer = CT * 4 / W;
   const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * R;
   const int64_t r_end = r_begin + R < n_rows ? r_begin + R : n_rows;
   // Head-sum pattern: A row m has ones at the k-slots of the heads of tile
@@ -718,7 +716,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   const uint32_t row_bytes = static_cast<uint32_t>(a.out_cols * sizeof(OutT));
 
   const int split = kSplit ? static_cast<int>(blockIdx.y) : 0;
-  constexpr int kChunkKeys = kStChunkTiles * 16;
+  constexpr int kChunkKeys = CT * 16;
   for (int64_t r = r_begin; r < r_end;) {
     const Segment sg = find_segment(a, r, r_end);
     const int64_t n = sg.end - r;
@@ -839,17 +837,17 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
       }
       u32x4 stage[kPer];
       __syncthreads();  // the previous user of kbuf is done
-      stream_issue<W>(kr, a.k_st, ch_lo, stage);
-      stream_commit<W>(kbuf[0], stage);
+      stream_issue<W, CT>(kr, a.k_st, ch_lo, stage);
+      stream_commit<W, CT>(kbuf[0], stage);
       __syncthreads();
       for (int ch = ch_lo; ch < ch_hi; ++ch) {
         const bf16x8* buf = kbuf[(ch - ch_lo) & 1];
-        if (ch + 1 < ch_hi) stream_issue<W>(kr, a.k_st, ch + 1, stage);
+        if (ch + 1 < ch_hi) stream_issue<W, CT>(kr, a.k_st, ch + 1, stage);
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
+        for (int qd = 0; qd < CT / 4; ++qd) {
           f32x4 acc[TW][4];
           stream_scores<TW>(buf, qd, qf, acc);
-          const int key0 = kStChunkTiles * 16 * ch + 64 * qd;  // first key of the quad
+          const int key0 = kChunkKeys * ch + 64 * qd;  // first key of the quad
           const bool masked = key0 + 64 > vis_min;              // wave-uniform
           if (pass == 0) {
             if (masked) {
@@ -975,7 +973,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             }
           }
         }
-        if (ch + 1 < ch_hi) stream_commit<W>(kbuf[(ch + 1 - ch_lo) & 1], stage);
+        if (ch + 1 < ch_hi) stream_commit<W, CT>(kbuf[(ch + 1 - ch_lo) & 1], stage);
         __syncthreads();
       }
       if (pass == 0) {
@@ -1497,11 +1495,12 @@ Stage1Path stage1_path(const Stage1Args& a) {
   return mfma ? kPathRowMfma : kPathGeneric;
 }
 
-// Key-split plan of the streaming path: pieces of 16 rows times splits of
-// `chunks` 256-key chunks, about four workgroups per CU in all (one runs per
-// CU at a time; fewer left CUs idle on decode batches, more gave splits of
-// one chunk, whose load is never overlapped); the workspace holds one float
-// per (piece, split, row, head).
+// Key-split plan of the streaming path: pieces of 8 rows (four waves of two
+// tokens) times splits of `chunks` 128-key chunks, about four workgroups per
+// CU in all (two run per CU at a time; fewer left CUs idle on decode
+// batches, more gave splits of one chunk, whose load is never overlapped);
+// the workspace holds one float per (piece, split, row, head).  A plan of
+// one split runs the whole-row kernel instead.
 struct SplitPlan {
   int64_t pieces;
   int32_t chunks, n_splits;
@@ -1509,7 +1508,7 @@ struct SplitPlan {
 };
 
 SplitPlan split_plan(int64_t n_rows, int64_t out_cols) {
-  constexpr int64_t R = kStWaves * kStTokensPerWave;
+  constexpr int64_t R = kStSplitWaves * kStTokensPerWave;
   constexpr int64_t kChunkKeys = kStChunkTiles * 16;
   SplitPlan p{};
   p.pieces = (n_rows + R - 1) / R;
@@ -1540,7 +1539,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
   if constexpr (kPool) {
     constexpr int kTW = kStTokensPerWave;
     const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
-    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, true, 0>),
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, true, 0>),
                        dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp,
                        Stage1Split{}, n_rows);
   } else if (path == kPathLds) {
@@ -1557,22 +1556,23 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
       default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
     }
   } else if (path == kPathStream) {
-    constexpr int kTW = kStTokensPerWave;
+    constexpr int kTW = kStTokensPerWave, kCT = kStChunkTiles;
     const SplitPlan plan = split_plan(n_rows, a.out_cols);
-    const dim3 block(kStWaves * kWave);
     if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes) {
       const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
       const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false, 1>), grid, block, 0, s,
-                         a, pp, sp, n_rows);
+      const dim3 block(kStSplitWaves * kWave);
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kCT, false, 1>), grid, block,
+                         0, s, a, pp, sp, n_rows);
       const int st = check_launch("infllmv2_attn_stage1");
       if (st != UNUM_OK) return st;
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false, 2>), grid, block, 0, s,
-                         a, pp, sp, n_rows);
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kCT, false, 2>), grid, block,
+                         0, s, a, pp, sp, n_rows);
     } else {
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, false, 0>),
-                         dim3(static_cast<unsigned>(plan.pieces)), block, 0, s, a, pp,
-                         Stage1Split{}, n_rows);
+      constexpr int64_t R = kStWaves * kTW;
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kCT, false, 0>),
+                         dim3(static_cast<unsigned>((n_rows + R - 1) / R)), dim3(kStWaves * kWave), 0,
+                         s, a, pp, Stage1Split{}, n_rows);
     }
   } else if (path == kPathRowMfma) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
