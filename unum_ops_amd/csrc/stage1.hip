@@ -586,13 +586,12 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
 // decode against a large cache).  A workgroup of W waves owns a piece of up
 // to W*TW consecutive tokens of one (sequence, group); wave w computes the
 // tokens w, w+W, ... (TW of them), so every K fragment read from LDS feeds TW
-// score MFMAs.  K streams through two LDS buffers in the fragment order of
-// the resident path, CT*16 keys at a time: the next chunk's loads are issued
-// into registers before the current chunk is computed and written to the free
-// buffer after it, with one barrier per chunk.  Whole rows run eight waves;
-// key splits (below) run four, with half the LDS, so that two workgroups
-// share a CU and one's loads overlap the other's compute (measured 40%
-// faster on decode batches; eight waves measured faster on long chunks).
+// score MFMAs.  K streams through a ring of NB LDS buffers in the fragment
+// order of the resident path, CT*16 keys at a time, loaded by buffer-to-LDS
+// loads NB-1 chunks ahead of the one being computed, with one barrier per
+// chunk.  Whole rows run eight waves; key splits (below) run four with a
+// third of the LDS, so that several workgroups share a CU (measured 40%
+// faster on decode batches; eight waves measured faster on long rows).
 //
 // The reference's two passes, with the VALU work per score kept to an fma, an
 // exp and one more op:
@@ -607,36 +606,74 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
 // Every quad of a streamed chunk is computed (keys past the visible range are
 // masked to 0), and stores past the row are dropped by the buffer range check,
 // so each chunk issues the same memory operations and waits stay exact.
-constexpr int kStChunkTiles = 8;           // 16-key tiles per streamed chunk (128 keys)
 constexpr float kStLimit = 18446744073709551616.f;  // 2^64
-constexpr int kStTokensPerWave = 2;  // tokens sharing each K fragment
-constexpr int kStWaves = 8;          // waves per workgroup on whole rows
-constexpr int kStSplitWaves = 4;     // waves per workgroup on key splits
+// Tokens sharing each K fragment: three (fewer LDS reads per MFMA) measured
+// no faster on long rows and slower on decode batches.
+constexpr int kStTokensPerWave = 2;
+// Whole rows: waves per workgroup, 16-key tiles per chunk, ring depth
+// (96 KiB of LDS, one workgroup per CU).
+constexpr int kStWaves = 8, kStChunkTiles = 8, kStRing = 3;
+// Key splits: 48 KiB of LDS and at most 168 VGPRs, so three workgroups share
+// a CU.
+constexpr int kStSplitWaves = 4, kStSplitTiles = 4, kStSplitRing = 3;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Issue the loads of chunk `ch` (keys CT*16*ch ..) of the piece's K block;
-// keys past the valid range read as zero (buffer range check).
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+constexpr int kDeadOffset = 0x7ffffff0;  // past every K range (< 2^31): reads zero
+
+// Buffer-to-LDS load of chunk `ch` (keys CT*16*ch ..) of the piece's K block
+// into `buf`, in fragment order: wave w loads the fragments f = w, w+W, ...
+// (16-key tile f/4, 32-column block f%4), each one 1 KiB run of LDS written
+// by one buffer_load ... lds.  Keys past the readable range, and every key of
+// a chunk that is not `live` (past the piece), read as zero through the
+// buffer range check, so every chunk issues the same loads.  The loads are
+// issued from inline assembly: the compiler cannot tell the ring's buffers
+// apart and would otherwise wait for every pending load before each LDS read
+// of the chunk being computed; the kernel waits for them itself.
 template <int W, int CT>
-__device__ __forceinline__ void stream_issue(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int ch,
-                                             u32x4 (&v)[CT * 4 / W]) {
-  int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid));
+__device__ __forceinline__ void stream_dma(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int ch, bool live,
+                                           const bf16x8* buf, int wave) {
+  const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
   for (int i = 0; i < CT * 4 / W; ++i) {
-    const int u = tid + i * W * kWave;
-    const int jt = u >> 8, cc = (u >> 6) & 3, l = u & 63;
-    const int key = CT * 16 * ch + 16 * jt + (l & 15);
-    const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (l >> 4)) * 2);
-    v[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
+    const int f = wave + i * W;
+    const int jt = f >> 2, cc = f & 3;
+    const int key = CT * 16 * ch + 16 * jt + (lane & 15);
+    const int off = live ? static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (lane >> 4)) * 2)
+                         : kDeadOffset;
+    const int m0 = __builtin_amdgcn_readfirstlane(
+        static_cast<int>(reinterpret_cast<uintptr_t>((lds_void_ptr)(buf + f * kWave))));
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(off), "s"(kr)
+                 : "memory", "m0");
   }
 }
-template <int W, int CT>
-__device__ __forceinline__ void stream_commit(bf16x8* buf, const u32x4 (&v)[CT * 4 / W]) {
-#pragma unroll
-  for (int i = 0; i < CT * 4 / W; ++i) {
-    const int u = static_cast<int>(threadIdx.x) + i * W * kWave;
-    buf[u] = __builtin_bit_cast(bf16x8, v[i]);
+
+// Wait until at most N of this wave's vector memory operations are pending
+// (they complete in issue order), then join the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// The wait before chunk k (0-based) of a pass: the chunk's loads are done
+// once at most Base + min(k, D) * S operations are pending -- the loads of
+// the D-1 chunks issued after it (Base) and the S stores of each chunk
+// computed since it was issued (at most D of them).
+template <int Base, int S, int D>
+__device__ __forceinline__ void chunk_wait(int k) {
+  if constexpr (S == 0) {
+    vm_wait_barrier<Base>();
+  } else if constexpr (D == 0) {
+    vm_wait_barrier<Base>();
+  } else {
+    if (k >= D)
+      vm_wait_barrier<Base + D * S>();
+    else
+      chunk_wait<Base, S, D - 1>(k);
   }
 }
 
@@ -686,19 +723,22 @@ struct Stage1Split {
   int32_t n_splits;
 };
 
-template <typename OutT, int W, int TW, int CT, bool kPool, int kSplit>
+template <typename OutT, int W, int TW, int CT, int NB, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
                                                                  Stage1Split sp, int64_t n_rows) {
   static_assert(!(kPool && kSplit), "the fused pool runs on whole rows");
-  static_assert((CT * 4) % W == 0, "every thread loads the same number of K units");
-  __shared__ bf16x8 kbuf[2][CT * 4 * kWave];
+  static_assert((CT * 4) % W == 0, "every wave loads the same number of K fragments");
+  static_assert(NB >= 2, "a ring of at least two chunks");
+  __shared__ bf16x8 kbuf[NB][CT * 4 * kWave];
+  constexpr int kAhead = NB - 1;                             // chunks in flight
+  constexpr int kLoads = CT * 4 / W;                         // loads per wave and chunk
+  constexpr int kStores = TW * (CT / 4) * (kPool ? 2 : 1);   // pass-2 stores per chunk
   // Wave-uniform by construction; readfirstlane lets the compiler keep the
   // per-token rows and store descriptors in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & (kWave - 1);
   const float c = a.scale_log2;  // > 0 on this path
   constexpr int R = W * TW;
-  constexpr int kPer = CT * 4 / W;
   const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * R;
   const int64_t r_end = r_begin + R < n_rows ? r_begin + R : n_rows;
   // Head-sum pattern: A row m has ones at the k-slots of the heads of tile
@@ -781,34 +821,6 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, k_bytes);
 
     float nb[TW][4];  // pass-2 bias: p = exp2(c*s + nb)
-    if constexpr (kSplit == 2) {
-      // Combine the splits' log2-sum-exps of each (row, head): lane group g
-      // reads heads 4g..4g+3 of the splits that hold visible keys.
-      const int64_t split_stride = static_cast<int64_t>(R) * 16;
-#pragma unroll
-      for (int k = 0; k < TW; ++k) {
-        const int ns = (vis[k] + sp.chunks * kChunkKeys - 1) / (sp.chunks * kChunkKeys);
-        const float* src = sp.ws + ws_row(k) + 4 * (lane >> 4);
-        float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        float sum[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int t = 0; t < ns; ++t) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(src + t * split_stride);
-          const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const float nm = fmaxf(m[rr], vv[rr]);
-            if (nm != -INFINITY) {
-              sum[rr] = sum[rr] * __builtin_amdgcn_exp2f(m[rr] - nm) +
-                        __builtin_amdgcn_exp2f(vv[rr] - nm);
-              m[rr] = nm;
-            }
-          }
-        }
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          nb[k][rr] = sum[rr] > 0.f ? -(m[rr] + __builtin_amdgcn_logf(sum[rr])) : -INFINITY;
-      }
-    }
     [[maybe_unused]] float carry_out[TW];  // fused pool: each token's last tap so far
 #pragma unroll
     for (int k = 0; k < TW; ++k) carry_out[k] = -INFINITY;
@@ -835,14 +847,60 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
         if constexpr (kPool)
           prsrc[k] = make_rsrc(pp.pooled + row * pp.nb, own[k] ? static_cast<uint32_t>(pp.nb * 4) : 0u);
       }
-      u32x4 stage[kPer];
       __syncthreads();  // the previous user of kbuf is done
-      stream_issue<W, CT>(kr, a.k_st, ch_lo, stage);
-      stream_commit<W, CT>(kbuf[0], stage);
-      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i)
+        stream_dma<W, CT>(kr, a.k_st, ch_lo + i, ch_lo + i < ch_hi, kbuf[i], wave);
+      if constexpr (kSplit == 2) {
+        // Combine the splits' log2-sum-exps of each (row, head): lane group g
+        // reads heads 4g..4g+3 of the splits that hold visible keys.
+        const int64_t split_stride = static_cast<int64_t>(R) * 16;
+#pragma unroll
+        for (int k = 0; k < TW; ++k) {
+          const int ns = (vis[k] + sp.chunks * kChunkKeys - 1) / (sp.chunks * kChunkKeys);
+          const float* src = sp.ws + ws_row(k) + 4 * (lane >> 4);
+          float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          float sum[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int t0 = 0; t0 < ns; t0 += 4) {  // four splits' loads in flight at once
+            f32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              v[u] = t0 + u < ns ? *reinterpret_cast<const f32x4*>(src + (t0 + u) * split_stride)
+                                 : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+              for (int rr = 0; rr < 4; ++rr) {
+                const float nm = fmaxf(m[rr], vv[rr]);
+                if (nm != -INFINITY) {
+                  sum[rr] = sum[rr] * __builtin_amdgcn_exp2f(m[rr] - nm) +
+                            __builtin_amdgcn_exp2f(vv[rr] - nm);
+                  m[rr] = nm;
+                }
+              }
+            }
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            nb[k][rr] = sum[rr] > 0.f ? -(m[rr] + __builtin_amdgcn_logf(sum[rr])) : -INFINITY;
+        }
+      }
+      // Take the queries (and split sums) here, while the first chunks load:
+      // the compiler does not count the ring's loads, so its own wait for
+      // them would otherwise come after the next chunk's loads are issued.
+#pragma unroll
+      for (int k = 0; k < TW; ++k)
+        asm volatile("" : : "v"(qf[k].v[0]), "v"(qf[k].v[1]), "v"(qf[k].v[2]), "v"(qf[k].v[3]));
       for (int ch = ch_lo; ch < ch_hi; ++ch) {
-        const bf16x8* buf = kbuf[(ch - ch_lo) & 1];
-        if (ch + 1 < ch_hi) stream_issue<W, CT>(kr, a.k_st, ch + 1, stage);
+        const int kc = ch - ch_lo;
+        if (pass == 0)
+          chunk_wait<(kAhead - 1) * kLoads, 0, kAhead>(kc);
+        else
+          chunk_wait<(kAhead - 1) * kLoads, kStores, kAhead>(kc);
+        // Every wave is past chunk ch-1, whose buffer takes chunk ch+kAhead.
+        stream_dma<W, CT>(kr, a.k_st, ch + kAhead, ch + kAhead < ch_hi, kbuf[(kc + kAhead) % NB], wave);
+        const bf16x8* buf = kbuf[kc % NB];
 #pragma unroll
         for (int qd = 0; qd < CT / 4; ++qd) {
           f32x4 acc[TW][4];
@@ -973,8 +1031,6 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             }
           }
         }
-        if (ch + 1 < ch_hi) stream_commit<W, CT>(kbuf[(ch + 1 - ch_lo) & 1], stage);
-        __syncthreads();
       }
       if (pass == 0) {
         // Combine the lanes' (reference, sum) into the row bias.
@@ -1032,6 +1088,9 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     }
     r = sg.end;
   }
+  // No buffer-to-LDS load may still be writing when the workgroup's LDS is
+  // released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // --------------------------------------------- LDS-resident K, pipelined rows
@@ -1066,8 +1125,6 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 // 2w+25), ... of a segment, each pair one short and one long row.
 constexpr int kRowSumLimit = 16384;  // 2^14: 1/sum is a normal f16
 constexpr int kRowWaves = 12;        // 768 threads: three waves per SIMD
-
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // K block of (sequence, group) -> LDS in fragment order (tiles [0, ntl)):
 // unit ((jt*4 + cc)*64 + l) = k[ks + 16*jt + l%16][g][32*cc + 8*(l/16) .. +8].
@@ -1496,9 +1553,9 @@ Stage1Path stage1_path(const Stage1Args& a) {
 }
 
 // Key-split plan of the streaming path: pieces of 8 rows (four waves of two
-// tokens) times splits of `chunks` 128-key chunks, about four workgroups per
-// CU in all (two run per CU at a time; fewer left CUs idle on decode
-// batches, more gave splits of one chunk, whose load is never overlapped);
+// tokens) times splits of `chunks` 64-key chunks, about four workgroups per
+// CU in all (fewer left CUs idle on decode batches, more cost more passes
+// over the split sums);
 // the workspace holds one float per (piece, split, row, head).  A plan of
 // one split runs the whole-row kernel instead.
 struct SplitPlan {
@@ -1509,7 +1566,7 @@ struct SplitPlan {
 
 SplitPlan split_plan(int64_t n_rows, int64_t out_cols) {
   constexpr int64_t R = kStSplitWaves * kStTokensPerWave;
-  constexpr int64_t kChunkKeys = kStChunkTiles * 16;
+  constexpr int64_t kChunkKeys = kStSplitTiles * 16;
   SplitPlan p{};
   p.pieces = (n_rows + R - 1) / R;
   const int64_t out_chunks = (out_cols + kChunkKeys - 1) / kChunkKeys;
@@ -1539,7 +1596,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
   if constexpr (kPool) {
     constexpr int kTW = kStTokensPerWave;
     const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
-    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, true, 0>),
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, true, 0>),
                        dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp,
                        Stage1Split{}, n_rows);
   } else if (path == kPathLds) {
@@ -1556,21 +1613,21 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
       default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
     }
   } else if (path == kPathStream) {
-    constexpr int kTW = kStTokensPerWave, kCT = kStChunkTiles;
+    constexpr int kTW = kStTokensPerWave;
     const SplitPlan plan = split_plan(n_rows, a.out_cols);
     if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes) {
       const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
       const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
       const dim3 block(kStSplitWaves * kWave);
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kCT, false, 1>), grid, block,
-                         0, s, a, pp, sp, n_rows);
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 1>),
+                         grid, block, 0, s, a, pp, sp, n_rows);
       const int st = check_launch("infllmv2_attn_stage1");
       if (st != UNUM_OK) return st;
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kCT, false, 2>), grid, block,
-                         0, s, a, pp, sp, n_rows);
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 2>),
+                         grid, block, 0, s, a, pp, sp, n_rows);
     } else {
       constexpr int64_t R = kStWaves * kTW;
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kCT, false, 0>),
+      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, false, 0>),
                          dim3(static_cast<unsigned>((n_rows + R - 1) / R)), dim3(kStWaves * kWave), 0,
                          s, a, pp, Stage1Split{}, n_rows);
     }
