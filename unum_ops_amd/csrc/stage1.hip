@@ -1015,14 +1015,15 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
                   p[u].w = ok ? p[u].w : 0.f;
                 }
               }
-              const f16x8 b01 = f16x8{static_cast<_Float16>(p[0].x), static_cast<_Float16>(p[0].y),
-                                      static_cast<_Float16>(p[0].z), static_cast<_Float16>(p[0].w),
-                                      static_cast<_Float16>(p[1].x), static_cast<_Float16>(p[1].y),
-                                      static_cast<_Float16>(p[1].z), static_cast<_Float16>(p[1].w)};
-              const f16x8 b23 = f16x8{static_cast<_Float16>(p[2].x), static_cast<_Float16>(p[2].y),
-                                      static_cast<_Float16>(p[2].z), static_cast<_Float16>(p[2].w),
-                                      static_cast<_Float16>(p[3].x), static_cast<_Float16>(p[3].y),
-                                      static_cast<_Float16>(p[3].z), static_cast<_Float16>(p[3].w)};
+              // f16 packs (rounded toward zero: one instruction per pair).
+              uint32_t pk[8];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                pk[2 * u] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[u].x, p[u].y));
+                pk[2 * u + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[u].z, p[u].w));
+              }
+              const f16x8 b01 = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+              const f16x8 b23 = __builtin_bit_cast(f16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
               f32x4 o = {0.f, 0.f, 0.f, 0.f};
               o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, o, 0, 0, 0);
               o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, o, 0, 0, 0);
