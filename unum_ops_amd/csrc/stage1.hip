@@ -469,7 +469,6 @@ __global__ __launch_bounds__(64) void stage1_generic_kernel(Stage1Args a) {
 // zig-zag; a workgroup's contiguous range of that order is cut into segments
 // of one (sequence, group) each (or of tokens outside every sequence).  The
 // LDS-resident kernel that walks them is further below.
-constexpr int kLdsWaves = 8;
 constexpr int kLdsTiles = 32;                    // 512 keys
 constexpr int kLdsUnits = kLdsTiles * 4 * kWave; // bf16x8 units: 128 KiB
 
@@ -561,6 +560,9 @@ __device__ Segment find_segment(const Stage1Args& a, int64_t r, int64_t r_end) {
   const int64_t seg_hi = static_cast<int64_t>(qs) * a.Hkv + static_cast<int64_t>(s.g + 1) * Lq;
   s.end = seg_hi < r_end ? seg_hi : r_end;
   if (s.end <= r) s.end = r + 1;
+  // A sequence reaching outside [0, Tq) (malformed cu_seqlens_q) is skipped,
+  // so no token indexes past q or the output.
+  if (qs < 0 || qe > a.Tq) s.kind = kSkip;
   return s;
 }
 
@@ -579,6 +581,97 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
     }
   }
   zero_tail<OutT>(orow, from, cols);
+}
+
+// ------------------------------------------------- pieces of the streaming path
+// The tokens of each (sequence, group) cut into blocks of R, numbered
+// sequence-major: sequence b owns Hkv*ceil(Lq_b/R) consecutive pieces, group-
+// major inside.  A workgroup finds its piece with a wave-level prefix sum over
+// cu_seqlens_q, 64 sequences per step; so no piece straddles two sequences.
+// Workgroups past the last piece zero the rows of tokens outside every
+// sequence.  A sequence reaching outside [0, Tq) (malformed cu_seqlens_q) has
+// its pieces skipped, so no token indexes past q or the output.
+constexpr int kStExtraGroups = 32;  // workgroups beyond the piece bound, for those rows
+
+struct Piece {
+  int32_t kind;        // SegKind
+  int32_t b, g;
+  int32_t qs, lq_len;  // the sequence's first token and length (the causal rule uses it)
+  int32_t ks, lk;      // its first compressed key and key count
+  int32_t t0, n;       // the piece's first token within the sequence, and its token count
+  int64_t extra, n_extra;  // kOrphan: this workgroup's index among those past the pieces
+};
+
+// Grid size: Hkv*(ceil(Tq/R) + B) bounds the piece count of a well-formed batch.
+__host__ __device__ inline int64_t piece_grid(int64_t Hkv, int64_t Tq, int64_t B, int R) {
+  return Hkv * ((Tq + R - 1) / R + B) + kStExtraGroups;
+}
+
+__device__ Piece find_piece(const Stage1Args& a, int64_t p, int R) {
+  const int lane = threadIdx.x & (kWave - 1);
+  Piece s{};
+  s.kind = kSkip;
+  s.n = 1;
+  int64_t before = 0;
+  for (int64_t base = 0; base < a.B; base += kWave) {
+    const int64_t b = base + lane;
+    int32_t cnt = 0;
+    if (b < a.B) {
+      const int32_t L = a.cu_q[b + 1] - a.cu_q[b];
+      cnt = L > 0 ? static_cast<int32_t>(a.Hkv) * ((L + R - 1) / R) : 0;
+    }
+    int32_t incl = cnt;  // inclusive prefix over the 64 lanes
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int32_t v = __shfl_up(incl, d);
+      incl += lane >= d ? v : 0;
+    }
+    const int32_t total = __builtin_amdgcn_readfirstlane(__shfl(incl, kWave - 1));
+    if (p < before + total) {
+      const uint64_t m = __ballot(before + incl > p);
+      const int l = static_cast<int>(__builtin_ctzll(m));
+      // Wave-uniform: the values below live in scalar registers.
+      const int64_t start = before + __builtin_amdgcn_readfirstlane(__shfl(incl - cnt, l));
+      const int32_t bb = static_cast<int32_t>(base + l);
+      const int32_t qs = a.cu_q[bb], qe = a.cu_q[bb + 1];
+      const int32_t L = qe - qs, nj = (L + R - 1) / R;
+      const int32_t off = static_cast<int32_t>(p - start);
+      s.b = bb;
+      s.g = off / nj;
+      s.t0 = (off - s.g * nj) * R;
+      s.n = L - s.t0 < R ? L - s.t0 : R;
+      s.qs = qs;
+      s.lq_len = L;
+      s.ks = a.cu_k[bb];
+      s.lk = a.cu_k[bb + 1] - s.ks;
+      s.kind = (qs >= 0 && qe <= a.Tq) ? kSeq : kSkip;
+      return s;
+    }
+    before += total;
+  }
+  s.kind = kOrphan;
+  s.extra = p - before;
+  s.n_extra = static_cast<int64_t>(gridDim.x) - before;
+  return s;
+}
+
+// Zero the rows of tokens outside every sequence -- [0, cu_q[0]) and
+// [cu_q[B], Tq), every group -- striding over the workgroups past the pieces.
+template <typename OutT, bool kPool>
+__device__ void zero_orphan_rows(const Stage1Args& a, const Stage1Pool& pp, const Piece& pc, int W) {
+  const int wave = static_cast<int>(threadIdx.x >> 6);
+  const int64_t lo = a.cu_q[0] < 0 ? 0 : (a.cu_q[0] > a.Tq ? a.Tq : a.cu_q[0]);
+  int64_t hi = a.cu_q[a.B] < lo ? lo : a.cu_q[a.B];
+  hi = hi > a.Tq ? a.Tq : hi;
+  const int64_t n_tok = lo + (a.Tq - hi);  // tokens before lo and from hi on
+  const int64_t n_rows = a.Hkv * n_tok;
+  for (int64_t r = pc.extra * W + wave; r < n_rows; r += pc.n_extra * W) {
+    const int64_t g = r / n_tok, i = r - g * n_tok;
+    const int64_t t = i < lo ? i : hi + (i - lo);
+    if (!kPool || pp.write_scores)
+      zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+    if constexpr (kPool) orphan_pool_row(pp, g * a.Tq + t);
+  }
 }
 
 // ------------------------------------------------------ K-streaming path
@@ -644,10 +737,14 @@ __device__ __forceinline__ void stream_dma(__amdgpu_buffer_rsrc_t kr, int64_t k_
                          : kDeadOffset;
     const int m0 = __builtin_amdgcn_readfirstlane(
         static_cast<int>(reinterpret_cast<uintptr_t>((lds_void_ptr)(buf + f * kWave))));
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(m0), "v"(off), "s"(kr)
-                 : "memory", "m0");
+    // M0 holds the LDS destination; the compiler's value of M0 is restored.
+    int saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(m0), "v"(off), "s"(kr)
+        : "memory");
   }
 }
 
@@ -739,8 +836,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   const int lane = threadIdx.x & (kWave - 1);
   const float c = a.scale_log2;  // > 0 on this path
   constexpr int R = W * TW;
-  const int64_t r_begin = static_cast<int64_t>(blockIdx.x) * R;
-  const int64_t r_end = r_begin + R < n_rows ? r_begin + R : n_rows;
+  (void)n_rows;
   // Head-sum pattern: A row m has ones at the k-slots of the heads of tile
   // u = m/4 (tiles 0,1 in wa, tiles 2,3 in wb), so lane group u of the result
   // holds tile u's per-key head sum.
@@ -757,27 +853,11 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 
   const int split = kSplit ? static_cast<int>(blockIdx.y) : 0;
   constexpr int kChunkKeys = CT * 16;
-  for (int64_t r = r_begin; r < r_end;) {
-    const Segment sg = find_segment(a, r, r_end);
-    const int64_t n = sg.end - r;
-    if (sg.kind == kOrphan) {
-      for (int64_t j = wave; j < n && kSplit != 1 && split == 0; j += W) {
-        const int64_t rel = r + j - sg.rlo;
-        const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
-        if (g < a.Hkv && t < a.Tq) {
-          if (!kPool || pp.write_scores)
-            zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
-          if constexpr (kPool) orphan_pool_row(pp, g * a.Tq + t);
-        }
-      }
-      r = sg.end;
-      continue;
-    }
-    if (sg.kind != kSeq) {
-      r = sg.end;
-      continue;
-    }
-    // Piece: tokens lq = k0 .. k0+n-1 of sequence b, group g (n <= R).
+  const Piece sg = find_piece(a, blockIdx.x, R);
+  if (sg.kind == kOrphan && kSplit != 1 && split == 0) zero_orphan_rows<OutT, kPool>(a, pp, sg, W);
+  if (sg.kind == kSeq) {
+    const int64_t n = sg.n;
+    // Piece: tokens lq = t0 .. t0+n-1 of sequence b, group g (n <= R).
     int32_t lq[TW], vis[TW];
     bool own[TW];
     auto vis_of = [&](int32_t q) -> int32_t {
@@ -793,13 +873,13 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     for (int k = 0; k < TW; ++k) {
       const int64_t i = wave + static_cast<int64_t>(W) * k;
       own[k] = i < n;
-      lq[k] = static_cast<int32_t>(sg.k0 + (own[k] ? i : n - 1));
+      lq[k] = static_cast<int32_t>(sg.t0 + (own[k] ? i : n - 1));
       vis[k] = vis_of(lq[k]);
       vis_min = vis[k] < vis_min ? vis[k] : vis_min;
     }
     // Causal visibility grows with the token, so the piece's last token sees
     // the most keys.
-    const int32_t kv_hi = vis_of(static_cast<int32_t>(sg.k0 + n - 1));
+    const int32_t kv_hi = vis_of(static_cast<int32_t>(sg.t0 + n - 1));
     const int nch = (kv_hi + kChunkKeys - 1) / kChunkKeys;
     // Chunks of this launch: all of them, or those of this key split.
     const int ch_lo = kSplit ? (split * sp.chunks < nch ? split * sp.chunks : nch) : 0;
@@ -808,7 +888,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     // token reads the row of the one it repeats).
     auto ws_row = [&](int k) -> int64_t {
       const int64_t i = own[k] ? wave + static_cast<int64_t>(W) * k : n - 1;
-      return ((static_cast<int64_t>(blockIdx.x) * sp.n_splits) * R + (r - r_begin) + i) * 16;
+      return ((static_cast<int64_t>(blockIdx.x) * sp.n_splits) * R + i) * 16;
     };
     Frag qf[TW];
 #pragma unroll
@@ -1059,16 +1139,12 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
         }
       }
     }
-    if constexpr (kSplit == 1) {
-      // Rows with no visible key in this split: the second pass reads only
-      // the splits below a row's visible count.
-      r = sg.end;
-      continue;
-    }
-    // Columns past the streamed chunks (of this split's columns).
+    // Columns past the streamed chunks (of this split's columns); the split
+    // sums of rows with no visible key in a split are not written: the
+    // second pass reads only the splits below a row's visible count.
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
-      if (own[k]) {
+      if (kSplit != 1 && own[k]) {
         const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq[k];
         int64_t done = static_cast<int64_t>(nch) * kChunkKeys;
         int64_t end = a.out_cols;
@@ -1087,7 +1163,6 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
         }
       }
     }
-    r = sg.end;
   }
   // No buffer-to-LDS load may still be writing when the workgroup's LDS is
   // released.
@@ -1565,11 +1640,11 @@ struct SplitPlan {
   int64_t bytes;
 };
 
-SplitPlan split_plan(int64_t n_rows, int64_t out_cols) {
-  constexpr int64_t R = kStSplitWaves * kStTokensPerWave;
+SplitPlan split_plan(int64_t Hkv, int64_t Tq, int64_t B, int64_t out_cols) {
+  constexpr int R = kStSplitWaves * kStTokensPerWave;
   constexpr int64_t kChunkKeys = kStSplitTiles * 16;
   SplitPlan p{};
-  p.pieces = (n_rows + R - 1) / R;
+  p.pieces = piece_grid(Hkv, Tq, B, R);
   const int64_t out_chunks = (out_cols + kChunkKeys - 1) / kChunkKeys;
   const int64_t target = 4 * static_cast<int64_t>(num_cus());
   int64_t chunks = (out_chunks * p.pieces + target - 1) / target;
@@ -1594,9 +1669,12 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
               "D=128, 16-byte aligned q/k and a positive scale (got G=%d, D=%d, %lld columns)",
               a.G, a.D, (long long)a.out_cols);
   const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
+  if (path == kPathStream && piece_grid(a.Hkv, a.Tq, a.B, kStSplitWaves * kStTokensPerWave) > INT32_MAX)
+    UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "infllmv2_attn_stage1: %lld tokens and %lld sequences are too many",
+              (long long)a.Tq, (long long)a.B);
   if constexpr (kPool) {
     constexpr int kTW = kStTokensPerWave;
-    const int64_t grid = (n_rows + kStWaves * kTW - 1) / (kStWaves * kTW);
+    const int64_t grid = piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW);
     hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, true, 0>),
                        dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp,
                        Stage1Split{}, n_rows);
@@ -1615,7 +1693,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
     }
   } else if (path == kPathStream) {
     constexpr int kTW = kStTokensPerWave;
-    const SplitPlan plan = split_plan(n_rows, a.out_cols);
+    const SplitPlan plan = split_plan(a.Hkv, a.Tq, a.B, a.out_cols);
     if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes) {
       const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
       const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
@@ -1627,10 +1705,9 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 2>),
                          grid, block, 0, s, a, pp, sp, n_rows);
     } else {
-      constexpr int64_t R = kStWaves * kTW;
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, false, 0>),
-                         dim3(static_cast<unsigned>((n_rows + R - 1) / R)), dim3(kStWaves * kWave), 0,
-                         s, a, pp, Stage1Split{}, n_rows);
+                         dim3(static_cast<unsigned>(piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW))),
+                         dim3(kStWaves * kWave), 0, s, a, pp, Stage1Split{}, n_rows);
     }
   } else if (path == kPathRowMfma) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
@@ -1652,12 +1729,11 @@ extern "C" int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t T
                                                             int64_t Hkv, int64_t D,
                                                             int64_t max_seqlen_k) {
   using namespace unum;
-  (void)B;
   // Only the streaming path (G = 16, D = 128, rows over 512 keys) splits keys.
   if (Tq <= 0 || Hkv <= 0 || Hq != kG * Hkv || D != kD || max_seqlen_k <= 0) return 0;
   const int64_t out_cols = (max_seqlen_k + 127) / 128 * 128;
   if (out_cols <= kLdsTiles * 16) return 0;
-  return split_plan(Hkv * Tq, out_cols).bytes;
+  return split_plan(Hkv, Tq, B, out_cols).bytes;
 }
 
 namespace unum {
