@@ -1628,10 +1628,11 @@ Stage1Path stage1_path(const Stage1Args& a) {
   return mfma ? kPathRowMfma : kPathGeneric;
 }
 
-// Key-split plan of the streaming path: pieces of 8 rows (four waves of two
-// tokens) times splits of `chunks` 64-key chunks, about four workgroups per
-// CU in all (fewer left CUs idle on decode batches, more cost more passes
-// over the split sums);
+// Key-split plan of the streaming path: pieces of 8 tokens (four waves of
+// two) times splits of `chunks` 64-key chunks, about six workgroups per CU in
+// all against the piece bound (measured on decode batches: four left CUs
+// idle, eight and more spent more on combining the splits; pieces of 4
+// tokens measured slower);
 // the workspace holds one float per (piece, split, row, head).  A plan of
 // one split runs the whole-row kernel instead.
 struct SplitPlan {
@@ -1646,7 +1647,7 @@ SplitPlan split_plan(int64_t Hkv, int64_t Tq, int64_t B, int64_t out_cols) {
   SplitPlan p{};
   p.pieces = piece_grid(Hkv, Tq, B, R);
   const int64_t out_chunks = (out_cols + kChunkKeys - 1) / kChunkKeys;
-  const int64_t target = 4 * static_cast<int64_t>(num_cus());
+  const int64_t target = 6 * static_cast<int64_t>(num_cus());
   int64_t chunks = (out_chunks * p.pieces + target - 1) / target;
   chunks = chunks < 1 ? 1 : chunks;
   const int64_t n_splits = out_chunks > 0 ? (out_chunks + chunks - 1) / chunks : 0;
