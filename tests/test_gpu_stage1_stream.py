@@ -111,6 +111,54 @@ def test_decode_mix_many_short_sequences(dev):
     _run_check(d, dev)
 
 
+@pytest.mark.parametrize("n_seq", [70, 150])
+def test_more_than_64_sequences_with_gaps(n_seq, dev):
+    # Workgroups find their piece from a prefix over cu_seqlens_q, 64
+    # sequences per step: batches past 64 sequences, empty sequences, and
+    # tokens outside every sequence (zeroed by the workgroups past the last
+    # piece), on the key-split kernels (short rows) and the whole-row kernel.
+    g = torch.Generator().manual_seed(49 + n_seq)
+    q_lens = torch.randint(0, 12, (n_seq,), generator=g).tolist()
+    q_lens[0], q_lens[-1] = 5, 17
+    ctx = torch.randint(8300, 9000, (n_seq,), generator=g).tolist()
+    d = workloads.stage1_inputs(q_lens, ctx, seed=49, raw_keys=False)
+    pre, post = 4, 7
+    d["q"] = torch.cat([torch.randn(pre, 32, 128).to(torch.bfloat16), d["q"],
+                        torch.randn(post, 32, 128).to(torch.bfloat16)])
+    d["cu_seqlens_q"] = d["cu_seqlens_q"] + pre
+    out = _run_check(d, dev)                       # with a workspace: key splits
+    assert float(out[:, :pre].abs().max()) == 0.0 and float(out[:, -post:].abs().max()) == 0.0
+    whole = _c_entry(d, dev, with_ws=False)        # without: the whole-row kernel
+    torch.testing.assert_close(whole.cpu(), out.cpu(), atol=1e-4, rtol=1e-3)
+    assert float(whole[:, :pre].abs().max()) == 0.0 and float(whole[:, -post:].abs().max()) == 0.0
+
+
+def _c_entry(d, dev, with_ws):
+    """Stage 1 through the C entry point, with or without the split workspace."""
+    import ctypes
+
+    from unum_ops_amd import _lib
+
+    q, k = d["q"].to(dev), d["k"].to(dev)
+    cu_q, cu_k = d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev)
+    B = cu_q.numel() - 1
+    cols = (d["max_seqlen_k"] + 127) // 128 * 128
+    lib = _lib.load()
+    ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(B, q.shape[0], 32, 2, 128,
+                                                            d["max_seqlen_k"])
+    out = torch.full((2, q.shape[0], cols), float("nan"), device=dev)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if with_ws else None
+    st = lib.unum_infllmv2_attn_stage1(
+        _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+        _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(out), _lib.UNUM_DTYPE_F32,
+        B, q.shape[0], k.shape[0], 32, 2, 128, d["max_seqlen_k"], cols,
+        ctypes.c_float(128 ** -0.5), 1, _lib.ptr(ws), ws_bytes if with_ws else 0,
+        _lib.stream_ptr(dev))
+    _lib.check(st, "stage1")
+    torch.cuda.synchronize()
+    return out
+
+
 @pytest.mark.parametrize("q_lens,ctx", [([40, 9], [9000, 30000]), ([300], [12000])])
 def test_workspace_absent_runs_the_unsplit_kernel(q_lens, ctx, dev):
     """The C entry point without a workspace runs the whole-row kernel; with one
