@@ -234,10 +234,28 @@ __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
 // ones with the lowest block ids, by a running rank.
 constexpr int kTopkMaxChunks = 16;  // NB <= 4096 (64 keys per lane)
 constexpr uint32_t kKeyNegInf = 0x007fffffu;  // order_key(-inf)
+constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t b = __float_as_uint(f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), d));
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), d));
+    v = o < v ? o : v;
+  }
+  return v;
 }
 
 // Lanes below this one whose bit is set in mask.
@@ -276,10 +294,36 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   int32_t need_eq = 0;  // blocks with key == tau to take, lowest ids first
   int32_t neg = 0;      // taken blocks scoring -inf
   if (NB > K) {
+    // Bounds on tau that fix its high bits: while fewer than K blocks are
+    // forced to +inf, tau is at most the largest finite key; and for K <= 64
+    // it is at least the smallest of the lanes' largest finite keys (64
+    // distinct keys lie at or above it).  tau shares every bit above the
+    // highest bit where the two differ, so the search starts there.  With
+    // one chunk (four keys a lane) the bounds cost more than the steps they
+    // save (measured).
+    int top = 31;
+    if (NCH >= 2 && K <= kWave && count_ge(kKeyPosInf) < K) {
+      uint32_t lmax = 0;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t k = key[ch][e] < kKeyPosInf ? key[ch][e] : 0u;
+          lmax = k > lmax ? k : lmax;
+        }
+      const uint32_t hi = wave_max_u32(lmax), lo = wave_min_u32(lmax);
+      if (lo == hi) {
+        top = -1;  // tau == hi
+        tau = hi;
+      } else {
+        top = 31 - __builtin_clz(lo ^ hi);
+        tau = hi & ~((2u << top) - 1u);  // the shared bits above `top`
+      }
+    }
     // A candidate with exactly K keys at or above it decides the selection
     // (keys >= it); the lower bits are then not needed, and the tie rule
     // below takes every key equal to it.
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = top; bit >= 0; --bit) {
       const uint32_t cand = tau | (1u << bit);
       const int32_t n = count_ge(cand);
       if (n >= K) tau = cand;
