@@ -60,6 +60,38 @@ def test_ties_everywhere(topk, dev):
     _check(d, dev, topk, **_kw(16384, 64 * 200, 2, 3))
 
 
+@pytest.mark.parametrize("topk", [1, 7, 64, 100])
+def test_ties_on_long_rows(topk, dev):
+    # 600 blocks (three chunks a lane): the search runs on the per-wave list
+    # of keys between its bounds; few distinct scores put ties at the cut.
+    d = workloads.maxpool_inputs([40, 25], F=2400, H=2, seed=11, k_lens=[2399, 1500])
+    x = d["input"]
+    d["input"] = torch.where(x > 0, torch.floor(x * 8192.0) / 16.0, x)
+    _check(d, dev, topk, **_kw(16 * 2400, 64 * 600, 1, 1))
+
+
+def test_most_keys_between_the_bounds(dev):
+    # Rows of one repeated score with a few larger ones: more than 512 keys
+    # lie between the bounds, so the search falls back to every key.
+    d = workloads.maxpool_inputs([30, 20], F=8448, H=2, seed=12, k_lens=[8447, 8000])
+    x = torch.full_like(d["input"], 0.25)
+    x[:, :, 1000:1003] = 0.75
+    x[:, 7:9, 5000] = 0.9
+    x[:, 30:, 8000:] = 0.0
+    d["input"] = x
+    _check(d, dev, 64, **_kw(16 * 8448, 64 * 2112))
+
+
+def test_minus_inf_blocks_on_long_rows(dev):
+    # Short key counts leave most of a 2112-block row at -inf.  With 38 or 10
+    # finite blocks some lanes hold only -inf, the bounds take every key and
+    # -inf blocks are selected (as -1); with 275 finite blocks every lane has
+    # one, and the -inf blocks stay below the short list's lower bound.
+    d = workloads.maxpool_inputs([20, 20, 20, 20], F=8448, H=2, seed=13,
+                                 k_lens=[8447, 150, 40, 1100])
+    _check(d, dev, 64, **_kw(16 * 8448, 64 * 2112))
+
+
 def test_fewer_blocks_than_topk(dev):
     d = workloads.maxpool_inputs([40, 9], F=128, H=2, seed=7, k_lens=[50, 20])
     _check(d, dev, 64, **_kw(2048, 1000))           # 16 blocks < 64

@@ -235,6 +235,7 @@ __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
 constexpr int kTopkMaxChunks = 16;  // NB <= 4096 (64 keys per lane)
 constexpr uint32_t kKeyNegInf = 0x007fffffu;  // order_key(-inf)
 constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)
+constexpr int kTopkShortList = 512;  // keys between the bounds kept per wave (8 a lane)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t b = __float_as_uint(f);
@@ -272,6 +273,7 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   const int lane = threadIdx.x & (kWave - 1);
   const RowCtx c = row_ctx(a, row);
   const int32_t NB = static_cast<int32_t>(a.NB);
+  __shared__ uint32_t short_list[4][kTopkShortList];  // one per wave of the 256-thread block
   // Keys of blocks n = 256*ch + 4*lane + e; 0 (below every real key) past NB.
   uint32_t key[NCH][4];
 #pragma unroll
@@ -302,7 +304,9 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
     // one chunk (four keys a lane) the bounds cost more than the steps they
     // save (measured).
     int top = 31;
-    if (NCH >= 2 && K <= kWave && count_ge(kKeyPosInf) < K) {
+    bool searched = false;
+    const int32_t n_inf = NCH >= 2 && K <= kWave ? count_ge(kKeyPosInf) : K;
+    if (n_inf < K) {
       uint32_t lmax = 0;
 #pragma unroll
       for (int ch = 0; ch < NCH; ++ch)
@@ -318,12 +322,55 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
       } else {
         top = 31 - __builtin_clz(lo ^ hi);
         tau = hi & ~((2u << top) - 1u);  // the shared bits above `top`
+        // Only keys in [lo, hi] (and the +inf ones, counted apart) can be at
+        // or above a candidate past lo: when at most kTopkShortList of them
+        // exist they go to a per-wave list in LDS, and the search counts
+        // that list -- eight keys a lane instead of 4*NCH.  At or below lo
+        // the list undercounts, but still holds at least 64 >= K keys, so
+        // the `>= K` decision stands; only the exact-K stop waits for a
+        // candidate past lo.
+        int32_t mine = 0;
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mine += (key[ch][e] >= lo && key[ch][e] <= hi) ? 1 : 0;
+        int32_t incl = mine;  // inclusive prefix over the lanes
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+          const int32_t v = __shfl_up(incl, d);
+          incl += lane >= d ? v : 0;
+        }
+        const int32_t total = __builtin_amdgcn_readfirstlane(__shfl(incl, kWave - 1));
+        if (total <= kTopkShortList) {
+          uint32_t* list = short_list[threadIdx.x >> 6];
+          int32_t pos = incl - mine;
+#pragma unroll
+          for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (key[ch][e] >= lo && key[ch][e] <= hi) list[pos++] = key[ch][e];
+          uint32_t sk[kTopkShortList / kWave];
+#pragma unroll
+          for (int i = 0; i < kTopkShortList / kWave; ++i) {
+            const int idx = i * kWave + lane;
+            sk[i] = idx < total ? list[idx] : 0u;  // 0 lies below every candidate
+          }
+          for (int bit = top; bit >= 0; --bit) {
+            const uint32_t cand = tau | (1u << bit);
+            int32_t n = n_inf;
+#pragma unroll
+            for (int i = 0; i < kTopkShortList / kWave; ++i) n += __popcll(__ballot(sk[i] >= cand));
+            if (n >= K) tau = cand;
+            if (n == K && cand > lo) break;
+          }
+          searched = true;
+        }
       }
     }
     // A candidate with exactly K keys at or above it decides the selection
     // (keys >= it); the lower bits are then not needed, and the tie rule
     // below takes every key equal to it.
-    for (int bit = top; bit >= 0; --bit) {
+    for (int bit = searched ? -1 : top; bit >= 0; --bit) {
       const uint32_t cand = tau | (1u << bit);
       const int32_t n = count_ge(cand);
       if (n >= K) tau = cand;
