@@ -1387,18 +1387,18 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
   const int lane = threadIdx.x & (kWave - 1);
   f16x8 wa, wb;
   {
-    float inv[4];
+    // The four weights as two f16 pairs (rounded to nearest: truncation would
+    // bias every row's sum low), placed whole dwords at a time: lanes of A
+    // row m hold them in the slots of tile m/4.
+    uint32_t wh[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) inv[r] = __builtin_amdgcn_rcpf(L[r]);
-    const int m = lane & 15;  // A row of this lane
-    const _Float16 h0 = static_cast<_Float16>(inv[0]), h1 = static_cast<_Float16>(inv[1]);
-    const _Float16 h2 = static_cast<_Float16>(inv[2]), h3 = static_cast<_Float16>(inv[3]);
-    const _Float16 z = static_cast<_Float16>(0.f);
-    const bool lo_a = m < 4, hi_a = m >= 4 && m < 8, lo_b = m >= 8 && m < 12, hi_b = m >= 12;
-    wa = f16x8{lo_a ? h0 : z, lo_a ? h1 : z, lo_a ? h2 : z, lo_a ? h3 : z,
-               hi_a ? h0 : z, hi_a ? h1 : z, hi_a ? h2 : z, hi_a ? h3 : z};
-    wb = f16x8{lo_b ? h0 : z, lo_b ? h1 : z, lo_b ? h2 : z, lo_b ? h3 : z,
-               hi_b ? h0 : z, hi_b ? h1 : z, hi_b ? h2 : z, hi_b ? h3 : z};
+    for (int r = 0; r < 4; ++r) wh[r] = f32_to_f16_bits(__builtin_amdgcn_rcpf(L[r]));
+    const uint32_t w01 = wh[0] | (wh[1] << 16), w23 = wh[2] | (wh[3] << 16);
+    const int t = (lane & 15) >> 2;  // the tile of this lane's A row
+    wa = __builtin_bit_cast(f16x8, u32x4{t == 0 ? w01 : 0u, t == 0 ? w23 : 0u,
+                                         t == 1 ? w01 : 0u, t == 1 ? w23 : 0u});
+    wb = __builtin_bit_cast(f16x8, u32x4{t == 2 ? w01 : 0u, t == 2 ? w23 : 0u,
+                                         t == 3 ? w01 : 0u, t == 3 ? w23 : 0u});
   }
 #pragma unroll
   for (int qd = 0; qd < kOutQ; ++qd) {
