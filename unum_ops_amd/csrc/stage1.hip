@@ -1302,19 +1302,17 @@ __device__ __forceinline__ void row_stage_exp(int j, const f32x4 (&s)[2], float 
   uint32_t pk[4];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].x, c, mc[0]));
-    float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].y, c, mc[1]));
-    float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].z, c, mc[2]));
-    float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].w, c, mc[3]));
-    if constexpr (kMasked) {
-      const bool ok = (lane & 15) < __builtin_amdgcn_readfirstlane(vis - 32 * j - 16 * u);
-      p0 = ok ? p0 : 0.f;
-      p1 = ok ? p1 : 0.f;
-      p2 = ok ? p2 : 0.f;
-      p3 = ok ? p3 : 0.f;
-    }
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].x, c, mc[0]));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].y, c, mc[1]));
+    const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].z, c, mc[2]));
+    const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u].w, c, mc[3]));
     pk[2 * u] = pk_f16(p0, p1);
     pk[2 * u + 1] = pk_f16(p2, p3);
+    if constexpr (kMasked) {  // the lane's key: one mask for all four heads (two packs)
+      const bool ok = (lane & 15) < __builtin_amdgcn_readfirstlane(vis - 32 * j - 16 * u);
+      pk[2 * u] = ok ? pk[2 * u] : 0u;
+      pk[2 * u + 1] = ok ? pk[2 * u + 1] : 0u;
+    }
   }
   const f16x8 v = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
   pw[j >> 1][j & 1] = v;
