@@ -822,7 +822,7 @@ struct Stage1Split {
 
 template <typename OutT, int W, int TW, int CT, int NB, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
-                                                                 Stage1Split sp, int64_t n_rows) {
+                                                                 Stage1Split sp) {
   static_assert(!(kPool && kSplit), "the fused pool runs on whole rows");
   static_assert((CT * 4) % W == 0, "every wave loads the same number of K fragments");
   static_assert(NB >= 2, "a ring of at least two chunks");
@@ -836,7 +836,6 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   const int lane = threadIdx.x & (kWave - 1);
   const float c = a.scale_log2;  // > 0 on this path
   constexpr int R = W * TW;
-  (void)n_rows;
   // Head-sum pattern: A row m has ones at the k-slots of the heads of tile
   // u = m/4 (tiles 0,1 in wa, tiles 2,3 in wb), so lane group u of the result
   // holds tile u's per-key head sum.
@@ -1676,7 +1675,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
     const int64_t grid = piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW);
     hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, true, 0>),
                        dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp,
-                       Stage1Split{}, n_rows);
+                       Stage1Split{});
   } else if (path == kPathLds) {
     int64_t grid = (n_rows + kRowWaves - 1) / kRowWaves;
     const int64_t cus = num_cus();
@@ -1698,15 +1697,15 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
       const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
       const dim3 block(kStSplitWaves * kWave);
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 1>),
-                         grid, block, 0, s, a, pp, sp, n_rows);
+                         grid, block, 0, s, a, pp, sp);
       const int st = check_launch("infllmv2_attn_stage1");
       if (st != UNUM_OK) return st;
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 2>),
-                         grid, block, 0, s, a, pp, sp, n_rows);
+                         grid, block, 0, s, a, pp, sp);
     } else {
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, false, 0>),
                          dim3(static_cast<unsigned>(piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW))),
-                         dim3(kStWaves * kWave), 0, s, a, pp, Stage1Split{}, n_rows);
+                         dim3(kStWaves * kWave), 0, s, a, pp, Stage1Split{});
     }
   } else if (path == kPathRowMfma) {
     const dim3 grid(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.Hkv));
