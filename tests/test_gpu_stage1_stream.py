@@ -111,6 +111,54 @@ def test_decode_mix_many_short_sequences(dev):
     _run_check(d, dev)
 
 
+# Decode batches (at most two new tokens per sequence on average, rows of at
+# most 4096 keys) run one workgroup per row, its waves splitting the keys.
+
+def test_decode_one_token_per_sequence(dev):
+    g = torch.Generator().manual_seed(61)
+    ctx = torch.randint(9000, 65000, (40,), generator=g).tolist()
+    d = workloads.stage1_inputs([1] * 40, ctx, seed=61, raw_keys=False)
+    _run_check(d, dev)
+
+
+def test_decode_ragged_with_gaps(dev):
+    # 0-3 new tokens per sequence, short and long rows (some under 64 keys),
+    # and tokens outside every sequence.
+    g = torch.Generator().manual_seed(62)
+    q_lens = torch.randint(0, 4, (90,), generator=g).tolist()
+    q_lens[0] = 3
+    ctx = torch.randint(200, 60000, (90,), generator=g).tolist()
+    ctx[1] = 40
+    d = workloads.stage1_inputs(q_lens, ctx, seed=62, raw_keys=False)
+    pre, post = 3, 5
+    d["q"] = torch.cat([torch.randn(pre, 32, 128).to(torch.bfloat16), d["q"],
+                        torch.randn(post, 32, 128).to(torch.bfloat16)])
+    d["cu_seqlens_q"] = d["cu_seqlens_q"] + pre
+    assert d["q"].shape[0] <= 2 * 90
+    out = _run_check(d, dev)
+    assert float(out[:, :pre].abs().max()) == 0.0 and float(out[:, -post:].abs().max()) == 0.0
+
+
+def test_decode_scores_far_above_the_first_quad(dev):
+    # Scores rise along the keys far above each wave's first quad: the
+    # reference moves (the quad is summed again).
+    Lk = 3900
+    q = torch.ones(2, 32, 128).to(torch.bfloat16)
+    ramp = (torch.arange(Lk, dtype=torch.float32) / Lk * 16.0)
+    k = ramp[:, None, None].expand(Lk, 2, 128).contiguous().to(torch.bfloat16)
+    d = dict(q=q, k=k, cu_seqlens_q=torch.tensor([0, 1, 2], dtype=torch.int32),
+             cu_seqlens_k=torch.tensor([0, Lk - 700, Lk], dtype=torch.int32), max_seqlen_k=Lk - 700)
+    out = _run_check(d, dev)
+    assert torch.isfinite(out).all()
+
+
+def test_decode_bf16_output_and_large_keys(dev):
+    d = workloads.stage1_inputs([1, 2, 1, 1], [30000, 20000, 9000, 50000], seed=63, raw_keys=False)
+    d["k"] = (d["k"].float() * 40.0).to(torch.bfloat16)
+    _run_check(d, dev)
+    _run_check(d, dev, out_dtype=torch.bfloat16)
+
+
 @pytest.mark.parametrize("n_seq", [70, 150])
 def test_more_than_64_sequences_with_gaps(n_seq, dev):
     # Workgroups find their piece from a prefix over cu_seqlens_q, 64

@@ -1168,6 +1168,220 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ------------------------------------------------------------- decode rows
+// For batches of about one new token per sequence (decode) over rows of at
+// most kDecMaxKeys keys: one workgroup of eight waves per (token, group) row,
+// the waves splitting the row's visible quads evenly.  A wave loads its keys
+// straight from global memory into registers (a quad's sixteen B fragments,
+// the next quad's loads issued before the current quad's MFMAs).  The two
+// passes of the streaming kernel run with the waves combining their
+// per-head (max, sum) through LDS between them; pass 2 re-reads the keys
+// (from L2).  No token slot repeats a token and no workspace is needed.
+constexpr int kDecWaves = 8;
+constexpr int kDecMaxKeys = 4096;  // longer rows take the streaming path
+
+struct QuadK {
+  bf16x8 f[4][4];  // [16-key tile u][32-column block cc]
+};
+
+// The sixteen K fragments of quad qd (keys 64*qd ..) of this lane; keys past
+// the readable range read as zero.
+__device__ __forceinline__ void dec_load(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int qd, QuadK& k) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int key = 64 * qd + 16 * u + (lane & 15);
+      const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (lane >> 4)) * 2);
+      k.f[u][cc] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+    }
+}
+
+__device__ __forceinline__ void dec_scores(const QuadK& k, const Frag& qf, f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf.v[cc], k.f[u][cc], acc[u], 0, 0, 0);
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kDecWaves* kWave) void stage1_decode_kernel(Stage1Args a) {
+  __shared__ float part_max[kDecWaves][kG];  // per wave and head: c * max (log2 domain)
+  __shared__ float part_sum[kDecWaves][kG];  // the sum of exp2 against it
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & (kWave - 1);
+  const float c = a.scale_log2;  // > 0 on this path
+  const Piece pc = find_piece(a, blockIdx.x, 1);
+  if (pc.kind == kOrphan) zero_orphan_rows<OutT, false>(a, Stage1Pool{}, pc, kDecWaves);
+  if (pc.kind != kSeq) return;  // workgroup-uniform
+  int32_t vis = pc.lk;
+  if (a.causal) {
+    vis = tdiv16(pc.t0 - 15) + pc.lk - tdiv16(pc.lq_len - 16 + 1);
+    vis = vis < 0 ? 0 : (vis > pc.lk ? pc.lk : vis);
+  }
+  vis = vis < a.out_cols ? vis : static_cast<int32_t>(a.out_cols);
+  const int nq = (vis + 63) >> 6;
+  const int q_lo = nq * wave / kDecWaves, q_hi = nq * (wave + 1) / kDecWaves;
+  const int64_t row = static_cast<int64_t>(pc.g) * a.Tq + pc.qs + pc.t0;
+  OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
+  // K block of (sequence, group): keys [0, keys_ok) are readable.
+  const int64_t keys_ok = pc.lk < a.Tk - pc.ks ? pc.lk : a.Tk - pc.ks;
+  const __bf16* kbase = a.k + static_cast<int64_t>(pc.ks) * a.k_st + static_cast<int64_t>(pc.g) * a.k_sh;
+  const __amdgpu_buffer_rsrc_t kr =
+      make_rsrc(kbase, keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u);
+  const Frag qf = load_q_frag(a, pc.qs + pc.t0, pc.g);
+
+  // Pass 1: per (lane, head) sums of exp2(c*s - c*mref) against the exact
+  // max of the wave's first quad, moved (the quad redone) only when a quad's
+  // sum exceeds 2^64.
+  float mref[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  float mc[4] = {0.f, 0.f, 0.f, 0.f}, l[4] = {0.f, 0.f, 0.f, 0.f};
+  QuadK kc, kn;
+  if (q_lo < q_hi) dec_load(kr, a.k_st, q_lo, kc);
+  for (int qd = q_lo; qd < q_hi; ++qd) {
+    if (qd + 1 < q_hi) dec_load(kr, a.k_st, qd + 1, kn);
+    f32x4 acc[4];
+    dec_scores(kc, qf, acc);
+    const int key0 = 64 * qd;
+    if (key0 + 64 > vis) {  // the row's last quad: keys at or past vis count as -inf
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool ok = key0 + 16 * u + (lane & 15) < vis;
+        acc[u].x = ok ? acc[u].x : -INFINITY;
+        acc[u].y = ok ? acc[u].y : -INFINITY;
+        acc[u].z = ok ? acc[u].z : -INFINITY;
+        acc[u].w = ok ? acc[u].w : -INFINITY;
+      }
+    }
+    float q4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    if (qd == q_lo) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        q4[0] = fmaxf(q4[0], acc[u].x);
+        q4[1] = fmaxf(q4[1], acc[u].y);
+        q4[2] = fmaxf(q4[2], acc[u].z);
+        q4[3] = fmaxf(q4[3], acc[u].w);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        mref[rr] = q4[rr];
+        mc[rr] = q4[rr] == -INFINITY ? 0.f : -c * q4[rr];
+      }
+    }
+    float le[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      le[0] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].x, c, mc[0]));
+      le[1] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].y, c, mc[1]));
+      le[2] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].z, c, mc[2]));
+      le[3] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].w, c, mc[3]));
+    }
+    bool big = false;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) big |= !(le[rr] <= kStLimit);
+    if (__builtin_amdgcn_ballot_w64(big) != 0) {
+      // Rare: a quad far above the reference.  The affected (lane, head)
+      // references move to the quad's exact max and the quad is summed again.
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        q4[0] = fmaxf(q4[0], acc[u].x);
+        q4[1] = fmaxf(q4[1], acc[u].y);
+        q4[2] = fmaxf(q4[2], acc[u].z);
+        q4[3] = fmaxf(q4[3], acc[u].w);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        if (!(le[rr] <= kStLimit)) {
+          const float nm = fmaxf(mref[rr], q4[rr]);
+          l[rr] = mref[rr] == -INFINITY ? 0.f : l[rr] * __builtin_amdgcn_exp2f((mref[rr] - nm) * c);
+          mref[rr] = nm;
+          mc[rr] = -c * nm;
+          float e = 0.f;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float sv = rr == 0 ? acc[u].x : rr == 1 ? acc[u].y : rr == 2 ? acc[u].z : acc[u].w;
+            e += __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, mc[rr]));
+          }
+          le[rr] = e;
+        }
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) l[rr] += le[rr];
+    kc = kn;
+  }
+  // The wave's per-head (c*max, sum), then the row's over the waves.
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const float M = grp_max16(mref[rr]);
+    const float part = mref[rr] == -INFINITY ? 0.f : l[rr] * __builtin_amdgcn_exp2f((mref[rr] - M) * c);
+    const float L = grp_sum16(part);
+    if ((lane & 15) == 0) {
+      part_max[wave][4 * (lane >> 4) + rr] = M == -INFINITY ? -INFINITY : M * c;
+      part_sum[wave][4 * (lane >> 4) + rr] = L;
+    }
+  }
+  __syncthreads();
+  float nb[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int h = 4 * (lane >> 4) + rr;
+    float Mg = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) Mg = fmaxf(Mg, part_max[w][h]);
+    float Lg = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w)
+      Lg += part_max[w][h] == -INFINITY ? 0.f : part_sum[w][h] * __builtin_amdgcn_exp2f(part_max[w][h] - Mg);
+    nb[rr] = Lg > 0.f ? -(Mg + __builtin_amdgcn_logf(Lg)) : -INFINITY;
+  }
+
+  // Pass 2: p = exp2(c*s + nb) is normalised; the head sum runs on an f16
+  // MFMA against a 0/1 pattern (lane group u of the result holds tile u's
+  // per-key sum, so lane i holds key 64*qd + i); one store per quad.
+  f16x8 wa, wb;
+  {
+    const int m = lane & 15;
+    const _Float16 one = static_cast<_Float16>(1.f), z = static_cast<_Float16>(0.f);
+    const _Float16 a0 = m < 4 ? one : z, a1 = (m >= 4 && m < 8) ? one : z;
+    const _Float16 b0 = (m >= 8 && m < 12) ? one : z, b1 = m >= 12 ? one : z;
+    wa = f16x8{a0, a0, a0, a0, a1, a1, a1, a1};
+    wb = f16x8{b0, b0, b0, b0, b1, b1, b1, b1};
+  }
+  const __amdgpu_buffer_rsrc_t orsrc =
+      make_rsrc(orow, static_cast<uint32_t>(a.out_cols * sizeof(OutT)));
+  if (q_lo < q_hi) dec_load(kr, a.k_st, q_lo, kc);
+  for (int qd = q_lo; qd < q_hi; ++qd) {
+    if (qd + 1 < q_hi) dec_load(kr, a.k_st, qd + 1, kn);
+    f32x4 acc[4];
+    dec_scores(kc, qf, acc);
+    const int key0 = 64 * qd;
+    uint32_t pk[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].x, c, nb[0]));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].y, c, nb[1]));
+      const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].z, c, nb[2]));
+      const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].w, c, nb[3]));
+      const bool ok = key0 + 16 * u + (lane & 15) < vis;
+      pk[2 * u] = ok ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1)) : 0u;
+      pk[2 * u + 1] = ok ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p2, p3)) : 0u;
+    }
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]}), o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, __builtin_bit_cast(f16x8, u32x4{pk[4], pk[5], pk[6], pk[7]}), o, 0, 0, 0);
+    buffer_store_out<OutT>(orsrc, (key0 + lane) * static_cast<int>(sizeof(OutT)), o.x);
+    kc = kn;
+  }
+  // Columns past the visible quads, spread over the waves.
+  for (int64_t j = static_cast<int64_t>(nq) * 64 + threadIdx.x; j < a.out_cols; j += kDecWaves * kWave)
+    store_out<OutT>(orow + j, 0.f);
+}
+
 // --------------------------------------------- LDS-resident K, pipelined rows
 // For sequences with at most kLdsTiles*16 = 512 compressed keys (the "32K"
 // prefill shapes).  One persistent workgroup of twelve waves per CU keeps the
@@ -1689,6 +1903,14 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
 #undef UNUM_LDS_CASE
       default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
     }
+  } else if (path == kPathStream && a.Tq <= 2 * a.B && a.out_cols <= kDecMaxKeys &&
+             (a.out_cols + 64) * a.k_st * 2 < (int64_t{1} << 31) &&
+             piece_grid(a.Hkv, a.Tq, a.B, 1) <= INT32_MAX) {
+    // Decode batches (at most two new tokens per sequence on average): one
+    // workgroup per row, the waves splitting its keys.
+    hipLaunchKernelGGL(stage1_decode_kernel<OutT>,
+                       dim3(static_cast<unsigned>(piece_grid(a.Hkv, a.Tq, a.B, 1))),
+                       dim3(kDecWaves * kWave), 0, s, a);
   } else if (path == kPathStream) {
     constexpr int kTW = kStTokensPerWave;
     const SplitPlan plan = split_plan(a.Hkv, a.Tq, a.B, a.out_cols);
@@ -1731,6 +1953,7 @@ extern "C" int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t T
   if (Tq <= 0 || Hkv <= 0 || Hq != kG * Hkv || D != kD || max_seqlen_k <= 0) return 0;
   const int64_t out_cols = (max_seqlen_k + 127) / 128 * 128;
   if (out_cols <= kLdsTiles * 16) return 0;
+  if (Tq <= 2 * B && out_cols <= kDecMaxKeys) return 0;  // decode batches: one workgroup per row
   return split_plan(Hkv, Tq, B, out_cols).bytes;
 }
 
