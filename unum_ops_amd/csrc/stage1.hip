@@ -1168,220 +1168,6 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// ------------------------------------------------------------- decode rows
-// For batches of about one new token per sequence (decode) over rows of at
-// most kDecMaxKeys keys: one workgroup of eight waves per (token, group) row,
-// the waves splitting the row's visible quads evenly.  A wave loads its keys
-// straight from global memory into registers (a quad's sixteen B fragments,
-// the next quad's loads issued before the current quad's MFMAs).  The two
-// passes of the streaming kernel run with the waves combining their
-// per-head (max, sum) through LDS between them; pass 2 re-reads the keys
-// (from L2).  No token slot repeats a token and no workspace is needed.
-constexpr int kDecWaves = 8;
-constexpr int kDecMaxKeys = 4096;  // longer rows take the streaming path
-
-struct QuadK {
-  bf16x8 f[4][4];  // [16-key tile u][32-column block cc]
-};
-
-// The sixteen K fragments of quad qd (keys 64*qd ..) of this lane; keys past
-// the readable range read as zero.
-__device__ __forceinline__ void dec_load(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int qd, QuadK& k) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int u = 0; u < 4; ++u)
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int key = 64 * qd + 16 * u + (lane & 15);
-      const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (lane >> 4)) * 2);
-      k.f[u][cc] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
-    }
-}
-
-__device__ __forceinline__ void dec_scores(const QuadK& k, const Frag& qf, f32x4 (&acc)[4]) {
-#pragma unroll
-  for (int u = 0; u < 4; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf.v[cc], k.f[u][cc], acc[u], 0, 0, 0);
-}
-
-template <typename OutT>
-__global__ __launch_bounds__(kDecWaves* kWave) void stage1_decode_kernel(Stage1Args a) {
-  __shared__ float part_max[kDecWaves][kG];  // per wave and head: c * max (log2 domain)
-  __shared__ float part_sum[kDecWaves][kG];  // the sum of exp2 against it
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int lane = threadIdx.x & (kWave - 1);
-  const float c = a.scale_log2;  // > 0 on this path
-  const Piece pc = find_piece(a, blockIdx.x, 1);
-  if (pc.kind == kOrphan) zero_orphan_rows<OutT, false>(a, Stage1Pool{}, pc, kDecWaves);
-  if (pc.kind != kSeq) return;  // workgroup-uniform
-  int32_t vis = pc.lk;
-  if (a.causal) {
-    vis = tdiv16(pc.t0 - 15) + pc.lk - tdiv16(pc.lq_len - 16 + 1);
-    vis = vis < 0 ? 0 : (vis > pc.lk ? pc.lk : vis);
-  }
-  vis = vis < a.out_cols ? vis : static_cast<int32_t>(a.out_cols);
-  const int nq = (vis + 63) >> 6;
-  const int q_lo = nq * wave / kDecWaves, q_hi = nq * (wave + 1) / kDecWaves;
-  const int64_t row = static_cast<int64_t>(pc.g) * a.Tq + pc.qs + pc.t0;
-  OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
-  // K block of (sequence, group): keys [0, keys_ok) are readable.
-  const int64_t keys_ok = pc.lk < a.Tk - pc.ks ? pc.lk : a.Tk - pc.ks;
-  const __bf16* kbase = a.k + static_cast<int64_t>(pc.ks) * a.k_st + static_cast<int64_t>(pc.g) * a.k_sh;
-  const __amdgpu_buffer_rsrc_t kr =
-      make_rsrc(kbase, keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u);
-  const Frag qf = load_q_frag(a, pc.qs + pc.t0, pc.g);
-
-  // Pass 1: per (lane, head) sums of exp2(c*s - c*mref) against the exact
-  // max of the wave's first quad, moved (the quad redone) only when a quad's
-  // sum exceeds 2^64.
-  float mref[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  float mc[4] = {0.f, 0.f, 0.f, 0.f}, l[4] = {0.f, 0.f, 0.f, 0.f};
-  QuadK kc, kn;
-  if (q_lo < q_hi) dec_load(kr, a.k_st, q_lo, kc);
-  for (int qd = q_lo; qd < q_hi; ++qd) {
-    if (qd + 1 < q_hi) dec_load(kr, a.k_st, qd + 1, kn);
-    f32x4 acc[4];
-    dec_scores(kc, qf, acc);
-    const int key0 = 64 * qd;
-    if (key0 + 64 > vis) {  // the row's last quad: keys at or past vis count as -inf
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const bool ok = key0 + 16 * u + (lane & 15) < vis;
-        acc[u].x = ok ? acc[u].x : -INFINITY;
-        acc[u].y = ok ? acc[u].y : -INFINITY;
-        acc[u].z = ok ? acc[u].z : -INFINITY;
-        acc[u].w = ok ? acc[u].w : -INFINITY;
-      }
-    }
-    float q4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    if (qd == q_lo) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        q4[0] = fmaxf(q4[0], acc[u].x);
-        q4[1] = fmaxf(q4[1], acc[u].y);
-        q4[2] = fmaxf(q4[2], acc[u].z);
-        q4[3] = fmaxf(q4[3], acc[u].w);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        mref[rr] = q4[rr];
-        mc[rr] = q4[rr] == -INFINITY ? 0.f : -c * q4[rr];
-      }
-    }
-    float le[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      le[0] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].x, c, mc[0]));
-      le[1] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].y, c, mc[1]));
-      le[2] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].z, c, mc[2]));
-      le[3] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].w, c, mc[3]));
-    }
-    bool big = false;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) big |= !(le[rr] <= kStLimit);
-    if (__builtin_amdgcn_ballot_w64(big) != 0) {
-      // Rare: a quad far above the reference.  The affected (lane, head)
-      // references move to the quad's exact max and the quad is summed again.
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        q4[0] = fmaxf(q4[0], acc[u].x);
-        q4[1] = fmaxf(q4[1], acc[u].y);
-        q4[2] = fmaxf(q4[2], acc[u].z);
-        q4[3] = fmaxf(q4[3], acc[u].w);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        if (!(le[rr] <= kStLimit)) {
-          const float nm = fmaxf(mref[rr], q4[rr]);
-          l[rr] = mref[rr] == -INFINITY ? 0.f : l[rr] * __builtin_amdgcn_exp2f((mref[rr] - nm) * c);
-          mref[rr] = nm;
-          mc[rr] = -c * nm;
-          float e = 0.f;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float sv = rr == 0 ? acc[u].x : rr == 1 ? acc[u].y : rr == 2 ? acc[u].z : acc[u].w;
-            e += __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, mc[rr]));
-          }
-          le[rr] = e;
-        }
-      }
-    }
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) l[rr] += le[rr];
-    kc = kn;
-  }
-  // The wave's per-head (c*max, sum), then the row's over the waves.
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const float M = grp_max16(mref[rr]);
-    const float part = mref[rr] == -INFINITY ? 0.f : l[rr] * __builtin_amdgcn_exp2f((mref[rr] - M) * c);
-    const float L = grp_sum16(part);
-    if ((lane & 15) == 0) {
-      part_max[wave][4 * (lane >> 4) + rr] = M == -INFINITY ? -INFINITY : M * c;
-      part_sum[wave][4 * (lane >> 4) + rr] = L;
-    }
-  }
-  __syncthreads();
-  float nb[4];
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int h = 4 * (lane >> 4) + rr;
-    float Mg = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) Mg = fmaxf(Mg, part_max[w][h]);
-    float Lg = 0.f;
-#pragma unroll
-    for (int w = 0; w < kDecWaves; ++w)
-      Lg += part_max[w][h] == -INFINITY ? 0.f : part_sum[w][h] * __builtin_amdgcn_exp2f(part_max[w][h] - Mg);
-    nb[rr] = Lg > 0.f ? -(Mg + __builtin_amdgcn_logf(Lg)) : -INFINITY;
-  }
-
-  // Pass 2: p = exp2(c*s + nb) is normalised; the head sum runs on an f16
-  // MFMA against a 0/1 pattern (lane group u of the result holds tile u's
-  // per-key sum, so lane i holds key 64*qd + i); one store per quad.
-  f16x8 wa, wb;
-  {
-    const int m = lane & 15;
-    const _Float16 one = static_cast<_Float16>(1.f), z = static_cast<_Float16>(0.f);
-    const _Float16 a0 = m < 4 ? one : z, a1 = (m >= 4 && m < 8) ? one : z;
-    const _Float16 b0 = (m >= 8 && m < 12) ? one : z, b1 = m >= 12 ? one : z;
-    wa = f16x8{a0, a0, a0, a0, a1, a1, a1, a1};
-    wb = f16x8{b0, b0, b0, b0, b1, b1, b1, b1};
-  }
-  const __amdgpu_buffer_rsrc_t orsrc =
-      make_rsrc(orow, static_cast<uint32_t>(a.out_cols * sizeof(OutT)));
-  if (q_lo < q_hi) dec_load(kr, a.k_st, q_lo, kc);
-  for (int qd = q_lo; qd < q_hi; ++qd) {
-    if (qd + 1 < q_hi) dec_load(kr, a.k_st, qd + 1, kn);
-    f32x4 acc[4];
-    dec_scores(kc, qf, acc);
-    const int key0 = 64 * qd;
-    uint32_t pk[8];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].x, c, nb[0]));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].y, c, nb[1]));
-      const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].z, c, nb[2]));
-      const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].w, c, nb[3]));
-      const bool ok = key0 + 16 * u + (lane & 15) < vis;
-      pk[2 * u] = ok ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p0, p1)) : 0u;
-      pk[2 * u + 1] = ok ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p2, p3)) : 0u;
-    }
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]}), o, 0, 0, 0);
-    o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, __builtin_bit_cast(f16x8, u32x4{pk[4], pk[5], pk[6], pk[7]}), o, 0, 0, 0);
-    buffer_store_out<OutT>(orsrc, (key0 + lane) * static_cast<int>(sizeof(OutT)), o.x);
-    kc = kn;
-  }
-  // Columns past the visible quads, spread over the waves.
-  for (int64_t j = static_cast<int64_t>(nq) * 64 + threadIdx.x; j < a.out_cols; j += kDecWaves * kWave)
-    store_out<OutT>(orow + j, 0.f);
-}
-
 // --------------------------------------------- LDS-resident K, pipelined rows
 // For sequences with at most kLdsTiles*16 = 512 compressed keys (the "32K"
 // prefill shapes).  One persistent workgroup of twelve waves per CU keeps the
@@ -1807,6 +1593,220 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
     }
     r = sg.end;
   }
+}
+
+// ------------------------------------------------------------- decode rows
+// For batches of about one new token per sequence (decode) over rows of at
+// most kDecMaxKeys keys: one workgroup of eight waves per (token, group) row,
+// the waves splitting the row's visible quads evenly.  A wave loads its keys
+// straight from global memory into registers (a quad's sixteen B fragments,
+// the next quad's loads issued before the current quad's MFMAs) and keeps
+// the row's f16 exponentials in LDS (128 KiB at most), as the resident
+// kernel keeps them in registers: one pass over the keys, then the waves
+// combine their per-head (reference, sum) and head-sum their exponentials
+// with weights 2^(c*mref - c*max) / sum.  No token slot repeats a token and
+// no workspace is needed.
+constexpr int kDecWaves = 8;
+constexpr int kDecMaxKeys = 4096;  // longer rows take the streaming path
+
+struct QuadK {
+  bf16x8 f[4][4];  // [16-key tile u][32-column block cc]
+};
+
+// The sixteen K fragments of quad qd (keys 64*qd ..) of this lane; keys past
+// the readable range read as zero.
+__device__ __forceinline__ void dec_load(__amdgpu_buffer_rsrc_t kr, int64_t k_st, int qd, QuadK& k) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int key = 64 * qd + 16 * u + (lane & 15);
+      const int off = static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (lane >> 4)) * 2);
+      k.f[u][cc] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+    }
+}
+
+__device__ __forceinline__ void dec_scores(const QuadK& k, const Frag& qf, f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf.v[cc], k.f[u][cc], acc[u], 0, 0, 0);
+}
+
+// Exponentials of quad qd of a decode row against the per-head reference mc
+// (keys at or past vis zeroed), packed to f16 in the B layout of the head-sum
+// MFMA (tiles 0,1 in v[0], tiles 2,3 in v[1]); their per-head sums go into
+// lsum through the 0/1 head selector `sel`.
+__device__ __forceinline__ void dec_exps(const f32x4 (&acc)[4], int key0, int32_t vis, float c,
+                                         const float (&mc)[4], f16x8 sel, f16x8 (&v)[2],
+                                         f32x4& lsum) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t pk[8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].x, c, mc[0]));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].y, c, mc[1]));
+    const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].z, c, mc[2]));
+    const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[u].w, c, mc[3]));
+    const bool ok = key0 + 16 * u + (lane & 15) < vis;
+    pk[2 * u] = ok ? pk_f16(p0, p1) : 0u;
+    pk[2 * u + 1] = ok ? pk_f16(p2, p3) : 0u;
+  }
+  v[0] = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+  v[1] = __builtin_bit_cast(f16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+  lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, v[0], lsum, 0, 0, 0);
+  lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, v[1], lsum, 0, 0, 0);
+}
+
+// Per head of the lane's group, the masked max of quad scores (acc) into m.
+__device__ __forceinline__ void dec_quad_max(const f32x4 (&acc)[4], int key0, int32_t vis,
+                                             float (&m)[4]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const bool ok = key0 + 16 * u + (lane & 15) < vis;
+    m[0] = fmaxf(m[0], ok ? acc[u].x : -INFINITY);
+    m[1] = fmaxf(m[1], ok ? acc[u].y : -INFINITY);
+    m[2] = fmaxf(m[2], ok ? acc[u].z : -INFINITY);
+    m[3] = fmaxf(m[3], ok ? acc[u].w : -INFINITY);
+  }
+}
+
+// One pass of a wave over its quads [q_lo, q_hi) of a decode row: the f16
+// exponentials against mc into the workgroup's LDS row, their per-head sums
+// into lsum.  With kFirst, mc is first taken from the wave's first quad (its
+// exact max over the 16 lanes of each head, so one reference per head).
+template <bool kFirst>
+__device__ __forceinline__ void dec_pass(__amdgpu_buffer_rsrc_t kr, int64_t k_st, const Frag& qf,
+                                         int q_lo, int q_hi, int32_t vis, float c, float (&mc)[4],
+                                         f16x8 sel, f16x8 (*erow)[2 * kWave], f32x4& lsum) {
+  const int lane = threadIdx.x & (kWave - 1);
+  lsum = f32x4{0.f, 0.f, 0.f, 0.f};
+  QuadK kc, kn;
+  if (q_lo < q_hi) dec_load(kr, k_st, q_lo, kc);
+  for (int qd = q_lo; qd < q_hi; ++qd) {
+    if (qd + 1 < q_hi) dec_load(kr, k_st, qd + 1, kn);
+    f32x4 acc[4];
+    dec_scores(kc, qf, acc);
+    if (kFirst && qd == q_lo) {
+      float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      dec_quad_max(acc, 64 * qd, vis, m);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mc[r] = -c * grp_max16(m[r]);  // a quad of the row has a visible key
+    }
+    f16x8 v[2];
+    dec_exps(acc, 64 * qd, vis, c, mc, sel, v, lsum);
+    erow[qd][lane] = v[0];
+    erow[qd][kWave + lane] = v[1];
+    kc = kn;
+  }
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kDecWaves* kWave) void stage1_decode_kernel(Stage1Args a) {
+  __shared__ f16x8 erow[kDecMaxKeys / 64][2 * kWave];  // the row's f16 exponentials: 128 KiB
+  __shared__ float part_max[kDecWaves][kG];  // per wave and head: c * reference
+  __shared__ float part_sum[kDecWaves][kG];  // the sum of exp2 against it
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & (kWave - 1);
+  const float c = a.scale_log2;  // > 0 on this path
+  const Piece pc = find_piece(a, blockIdx.x, 1);
+  if (pc.kind == kOrphan) zero_orphan_rows<OutT, false>(a, Stage1Pool{}, pc, kDecWaves);
+  if (pc.kind != kSeq) return;  // workgroup-uniform
+  int32_t vis = pc.lk;
+  if (a.causal) {
+    vis = tdiv16(pc.t0 - 15) + pc.lk - tdiv16(pc.lq_len - 16 + 1);
+    vis = vis < 0 ? 0 : (vis > pc.lk ? pc.lk : vis);
+  }
+  vis = vis < a.out_cols ? vis : static_cast<int32_t>(a.out_cols);
+  const int nq = (vis + 63) >> 6;
+  const int q_lo = nq * wave / kDecWaves, q_hi = nq * (wave + 1) / kDecWaves;
+  const int64_t row = static_cast<int64_t>(pc.g) * a.Tq + pc.qs + pc.t0;
+  OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
+  // K block of (sequence, group): keys [0, keys_ok) are readable.
+  const int64_t keys_ok = pc.lk < a.Tk - pc.ks ? pc.lk : a.Tk - pc.ks;
+  const __bf16* kbase = a.k + static_cast<int64_t>(pc.ks) * a.k_st + static_cast<int64_t>(pc.g) * a.k_sh;
+  const __amdgpu_buffer_rsrc_t kr =
+      make_rsrc(kbase, keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u);
+  const Frag qf = load_q_frag(a, pc.qs + pc.t0, pc.g);
+  // Per-head sum selector (A operand): row m has ones at the k-slots of head
+  // m in both tiles of a half.
+  f16x8 sel;
+  {
+    const int m = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) sel[jj] = static_cast<_Float16>(4 * g + (jj & 3) == m ? 1.f : 0.f);
+  }
+
+  // One pass over the keys: f16 exponentials against the exact max of the
+  // wave's first quad, kept in LDS.  Every head's sum at most 2^14 proves
+  // that no f16 value overflowed; a wave that fails it (a later key far
+  // above its first quad) redoes its quads against their exact max.
+  float mc[4];
+  f32x4 lsum;
+  dec_pass<true>(kr, a.k_st, qf, q_lo, q_hi, vis, c, mc, sel, erow, lsum);
+  float L[4];
+  if (q_lo < q_hi && !row_sums(lsum, L)) {
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    QuadK kc;
+    for (int qd = q_lo; qd < q_hi; ++qd) {
+      dec_load(kr, a.k_st, qd, kc);
+      f32x4 acc[4];
+      dec_scores(kc, qf, acc);
+      dec_quad_max(acc, 64 * qd, vis, m);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mc[r] = -c * grp_max16(m[r]);
+    dec_pass<false>(kr, a.k_st, qf, q_lo, q_hi, vis, c, mc, sel, erow, lsum);
+    row_sums(lsum, L);
+  }
+  // The row's per-head (max, sum) over the waves.
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      part_max[wave][4 * (lane >> 4) + rr] = q_lo < q_hi ? -mc[rr] : -INFINITY;
+      part_sum[wave][4 * (lane >> 4) + rr] = q_lo < q_hi ? L[rr] : 0.f;
+    }
+  }
+  __syncthreads();
+  if (q_lo < q_hi) {
+    // Head-sum weights of this wave's exponentials: 2^(c*mref - c*max) / sum
+    // for the heads of the lane's group, placed as in the resident kernel.
+    uint32_t wh[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int h = 4 * (lane >> 4) + rr;
+      float Mg = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) Mg = fmaxf(Mg, part_max[w][h]);
+      float Lg = 0.f;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w)
+        Lg += part_max[w][h] == -INFINITY ? 0.f : part_sum[w][h] * __builtin_amdgcn_exp2f(part_max[w][h] - Mg);
+      wh[rr] = f32_to_f16_bits(__builtin_amdgcn_exp2f(-mc[rr] - Mg) * __builtin_amdgcn_rcpf(Lg));
+    }
+    const uint32_t w01 = wh[0] | (wh[1] << 16), w23 = wh[2] | (wh[3] << 16);
+    const int t = (lane & 15) >> 2;  // the tile of this lane's A row
+    const f16x8 wa = __builtin_bit_cast(f16x8, u32x4{t == 0 ? w01 : 0u, t == 0 ? w23 : 0u,
+                                                     t == 1 ? w01 : 0u, t == 1 ? w23 : 0u});
+    const f16x8 wb = __builtin_bit_cast(f16x8, u32x4{t == 2 ? w01 : 0u, t == 2 ? w23 : 0u,
+                                                     t == 3 ? w01 : 0u, t == 3 ? w23 : 0u});
+    const __amdgpu_buffer_rsrc_t orsrc =
+        make_rsrc(orow, static_cast<uint32_t>(a.out_cols * sizeof(OutT)));
+    for (int qd = q_lo; qd < q_hi; ++qd) {
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, erow[qd][lane], o, 0, 0, 0);
+      o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, erow[qd][kWave + lane], o, 0, 0, 0);
+      buffer_store_out<OutT>(orsrc, (64 * qd + lane) * static_cast<int>(sizeof(OutT)), o.x);
+    }
+  }
+  // Columns past the visible quads, spread over the waves.
+  for (int64_t j = static_cast<int64_t>(nq) * 64 + threadIdx.x; j < a.out_cols; j += kDecWaves * kWave)
+    store_out<OutT>(orow + j, 0.f);
 }
 
 int num_cus() {
