@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
                                        "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
                                        "compress_keys_cfg5", "stage1_maxpool",
-                                       "stage1_maxpool_cfg5", "stage1_cfg4", "copy"],
+                                       "stage1_maxpool_cfg5", "stage1_cfg4", "stage1_decode",
+                                       "copy"],
                     default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
@@ -96,6 +97,12 @@ def build_inputs(dev):
               cu_k=p4["cu_seqlens_k"].to(dev), max_seqlen_k=p4["max_seqlen_k"],
               cu_q_cpu=p4["cu_seqlens_q"], cu_k_cpu=p4["cu_seqlens_k"])
     c5["cfg4"] = c4
+    # Pure decode (not a BASELINE config; the serving shape the decode kernel
+    # is for): 64 sequences of one new token after 32768 cached tokens.
+    pd = workloads.pipeline_inputs([1] * 64, [32768] * 64, raw_keys=False)
+    c5["decode"] = dict(q=pd["q"].to(dev), k=pd["k"].to(dev), cu_q=pd["cu_seqlens_q"].to(dev),
+                        cu_k=pd["cu_seqlens_k"].to(dev), max_seqlen_k=pd["max_seqlen_k"],
+                        cu_q_cpu=pd["cu_seqlens_q"], cu_k_cpu=pd["cu_seqlens_k"])
     torch.cuda.synchronize()
     log(f"cfg4/cfg5 inputs ready ({time.time() - t0:.1f}s)")
     return s1, s1g, mp, mpg, bt, c5
@@ -178,6 +185,12 @@ def main():
         return infllmv2_attn_stage1(c4["q"], c4["k"], None, c4["cu_q"], c4["cu_k"],
                                     max_seqlen_k=c4["max_seqlen_k"], causal=True)
 
+    cd = c5["decode"]
+
+    def op_stage1_decode():
+        return infllmv2_attn_stage1(cd["q"], cd["k"], None, cd["cu_q"], cd["cu_k"],
+                                    max_seqlen_k=cd["max_seqlen_k"], causal=True)
+
     def op_compress_cfg5():
         return compress_keys(c5["raw"], c5["cu_raw"], plan=plan5)
 
@@ -188,7 +201,8 @@ def main():
     extra = [("stage1_cfg5", op_stage1_cfg5), ("maxpool_cfg5", op_maxpool_cfg5),
              ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5),
              ("compress_keys_cfg5", op_compress_cfg5), ("stage1_maxpool", op_stage1_maxpool),
-             ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5), ("stage1_cfg4", op_stage1_cfg4)]
+             ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5), ("stage1_cfg4", op_stage1_cfg4),
+             ("stage1_decode", op_stage1_decode)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -274,6 +288,17 @@ def main():
                                     config=f"cfg4 64 sequences, 1-16 new tokens after 16K-64K "
                                            f"cached, Hq32/Hkv2/D128, fp32 out "
                                            f"[2,{int(c4['cu_q_cpu'][-1])},{ncols}]")
+    if "stage1_decode" in per_op:
+        ncols = -(-cd["max_seqlen_k"] // 128) * 128
+        flop, nbytes, _ = workloads.stage1_work(cd["cu_q_cpu"], cd["cu_k_cpu"], 32, 2, 128, ncols)
+        t = per_op["stage1_decode"] * 1e-3
+        comps["stage1_decode"] = dict(us=per_op["stage1_decode"] * 1e3, tflops=flop / t / 1e12,
+                                      gbs=nbytes / t / 1e9,
+                                      pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                      flop=flop, bytes=nbytes, bound="hbm",
+                                      config=f"decode: 64 sequences of 1 new token after 32768 "
+                                             f"cached, Hq32/Hkv2/D128, fp32 out [2,64,{ncols}] "
+                                             f"(not a BASELINE config)")
     if "maxpool_cfg5" in per_op:
         nbytes = workloads.maxpool_bytes(c5["cu_q_cpu"], c5["cu_k_cpu"], [0], 2,
                                          -(-c5["max_context_len"] // 64))
