@@ -67,16 +67,20 @@ int unum_abi_version(void);
  *   out[g, t, j] = sum_{i<G} softmax_j(scale * q[t, gG+i] . k[cu_k[b]+j, g])
  * over the visible keys j < vis(t) (causal rule of the reference, truncating
  * division), 0 for vis <= j < out_cols, and 0 for the whole row when
- * vis == 0 or the sequence has no keys.  Every element of `out` is written;
- * keys of a sequence at j >= out_cols are not (the reference writes past the
- * row there).
+ * vis == 0 or the sequence has no keys.  Every element of `out` is written
+ * when cu_seqlens_q is non-decreasing within [0, Tq]; keys of a sequence at
+ * j >= out_cols are not (the reference writes past the row there).  The rows
+ * of a sequence reaching outside [0, Tq) (malformed cu_seqlens_q) are left
+ * unwritten, never indexed.
  *
  * `workspace` (device memory, caller-owned, no initial contents needed) of
  * unum_infllmv2_attn_stage1_workspace_size(...) bytes lets rows over 512 keys
  * split their keys between workgroups (two launches on `stream`: per-split
  * log-sum-exps, then the scores); NULL or a smaller workspace runs the
- * whole-row kernel, with the same results to within fp32 rounding.  Calls that
- * share one workspace must not overlap.
+ * whole-row kernel, with the same results to within fp32 rounding.  Batches
+ * of at most two new tokens per sequence over rows of at most 4096 keys run
+ * one workgroup per row and need no workspace.  Calls that share one
+ * workspace must not overlap.
  */
 int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                               const void* k, int64_t k_stride_t, int64_t k_stride_h,
@@ -89,7 +93,7 @@ int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_strid
 
 /* Workspace bytes unum_infllmv2_attn_stage1 uses for this problem on the
  * current device (>= 0; 0: the problem is not split), with out_cols =
- * round_up(max_seqlen_k, 128). */
+ * round_up(max_seqlen_k, 128).  B is the number of sequences. */
 int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t Hq,
                                                  int64_t Hkv, int64_t D,
                                                  int64_t max_seqlen_k);

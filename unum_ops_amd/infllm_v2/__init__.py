@@ -89,7 +89,8 @@ def infllmv2_attn_stage1(q, k, v, cu_seqlens_q, cu_seqlens_k, cu_seqlens_v=None,
     lib = _lib.load()
     with torch.cuda.device(dev):
         # Rows over 512 keys split their keys between workgroups through a
-        # small workspace (about 1 KiB per 16 rows and split).
+        # small workspace (about 1 KiB per 16 rows and split); decode
+        # batches run one workgroup per row and need none.
         ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(
             batch, total_q, n_heads, n_kv_heads, head_dim, max_seqlen_k)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
