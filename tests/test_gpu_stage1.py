@@ -160,3 +160,60 @@ def test_odd_lengths_and_pair_split(q_lens, dev):
     ctx = [16 * q + 900 for q in q_lens]
     d = workloads.stage1_inputs(q_lens, ctx, seed=sum(q_lens))
     _check(d, _run(d, dev))
+
+
+def _c_entry_nan(d, dev):
+    """Stage 1 through the C entry point into an output that starts as NaN."""
+    import ctypes
+
+    from unum_ops_amd import _lib
+
+    q, k = d["q"].to(dev), d["k"].to(dev)
+    cu_q, cu_k = d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev)
+    cols = (d["max_seqlen_k"] + 127) // 128 * 128
+    out = torch.full((2, q.shape[0], cols), float("nan"), device=dev)
+    lib = _lib.load()
+    st = lib.unum_infllmv2_attn_stage1(
+        _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+        _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(out), _lib.UNUM_DTYPE_F32,
+        cu_q.numel() - 1, q.shape[0], k.shape[0], 32, 2, 128, d["max_seqlen_k"], cols,
+        ctypes.c_float(128 ** -0.5), 1, None, 0, _lib.stream_ptr(dev))
+    _lib.check(st, "stage1")
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("n_seq", [70, 150])
+def test_many_sequences_with_gaps(n_seq, dev):
+    """Rows of at most 512 keys: workgroups walk pieces of eight tokens across
+    more than 64 sequences, sequences without tokens, a sequence without keys,
+    and tokens outside every sequence (zero rows).  The output starts as NaN,
+    so an element left unwritten fails the comparison."""
+    g = torch.Generator().manual_seed(50 + n_seq)
+    q_lens = torch.randint(0, 40, (n_seq,), generator=g).tolist()
+    q_lens[0], q_lens[-1], q_lens[3] = 5, 17, 0
+    ctx = torch.randint(40, 8000, (n_seq,), generator=g).tolist()
+    ctx[1] = 8          # no compressed key: an all-zero row for each token
+    d = workloads.stage1_inputs(q_lens, ctx, seed=50)
+    assert d["max_seqlen_k"] <= 512
+    pre, post = 3, 6
+    d["q"] = torch.cat([torch.randn(pre, 32, 128).to(torch.bfloat16), d["q"],
+                        torch.randn(post, 32, 128).to(torch.bfloat16)])
+    d["cu_seqlens_q"] = d["cu_seqlens_q"] + pre
+    out = _c_entry_nan(d, dev)
+    assert not torch.isnan(out).any()
+    assert float(out[:, :pre].abs().max()) == 0.0 and float(out[:, -post:].abs().max()) == 0.0
+    _check(d, out)
+
+
+@pytest.mark.parametrize("split", [64, 256])
+def test_key_halves_far_apart(split, dev):
+    """Keys from `split` on scaled far up: the waves that share a row's keys then
+    hold references far apart, and the one below gets tiny head-sum weights."""
+    d = workloads.stage1_inputs([700, 301], [8192, 6000], seed=26)
+    k = d["k"].float()
+    cu_k = d["cu_seqlens_k"].tolist()
+    for b in range(2):
+        k[cu_k[b] + split:cu_k[b + 1]] *= 12.0
+    d["k"] = k.to(torch.bfloat16)
+    _check(d, _run(d, dev))
