@@ -1180,17 +1180,18 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 // measured faster than eight (which leave room for more registers) and than
 // sixteen (which spill).
 //
-// Softmax with one exp per score: the exponentials are taken against the
-// exact max of the row's first 64-key quad (a reference, not the row max) and
-// kept in registers as f16 (rounded toward zero) until the row is done.  The
+// Softmax with one exp per score: the exponentials are taken against each
+// head's score of key 0 (a reference, not the row max; its exponential is 1,
+// so every per-head sum is at least 1) and kept in registers as f16 (rounded
+// toward zero) until the row is done.  The
 // per-head sums and the final head sum both run on the matrix core: every
 // half-quad's f16 pack is multiplied by a 0/1 head selector into a per-head
 // accumulator, and at the end by the heads' 1/sum weights into the output.
 // Every exponential is positive, so a head's sum bounds each of its values:
 // one check per row -- every head's sum at most 2^14 -- proves that no f16
 // value overflowed and that every weight is a normal f16.  A row that fails
-// it (a later key far above the first quad's max) is redone against its
-// exact max, where the sums lie in [1, 512].
+// it (a later key far above key 0) is redone against its exact max, where
+// the sums lie in [1, 512].
 //
 // Work split: the (group, token) rows of the batch are ordered by sequence,
 // then group, then token in zig-zag order (0, L-1, 1, L-2, ...), and each
@@ -1411,7 +1412,7 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
 }
 
 // Per-head sums of a row from the accumulated selector MFMAs; false when one
-// exceeds 2^14 (the first-quad reference was too low for f16).
+// exceeds 2^14 (the key-0 reference was too low for f16).
 __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
   const float lv[4] = {lsum.x, lsum.y, lsum.z, lsum.w};
   bool bad = false;
@@ -1423,11 +1424,20 @@ __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
   return __builtin_amdgcn_ballot_w64(bad) == 0;
 }
 
+// Lane 16*(l/16) of v, for every lane l: DPP row_newbcast:0 (gfx90a and later).
+__device__ __forceinline__ float row_lane0(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
+}
+
 // A row of exactly NQ visible quads, as one straight-line block: the scores,
-// the reference max from quad 0, the exponentials and their per-head sums,
+// the exponentials against a per-head reference and their per-head sums,
 // quad by quad (the compiler interleaves one quad's MFMAs with the previous
-// quad's exponentials); only the last quad is masked.  Returns false, having
-// stored nothing, when the row needs its exact max.
+// quad's exponentials); only the last quad is masked.  The reference is each
+// head's score of key 0 -- visible in every row with a quad, lane 16g of
+// tile 0 holding it for heads 4g..4g+3 -- so every per-head sum is at least
+// its exponential, 1; a later key more than 14 binary orders above it fails
+// the 2^14 check instead.  Returns false, having stored nothing, when the row
+// needs its exact max.
 template <typename OutT, int NQ, int kOutQ>
 __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, float c, f16x8 sel,
                                          OutT* orow) {
@@ -1438,10 +1448,10 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
     f32x4 sa[2], sb[2];
     row_half_mfma(kl, 0, qf, sa);
     row_half_mfma(kl, 1, qf, sb);
-    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    row_quad_max<NQ == 1>(sa, sb, 0, vis, m);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mc[r] = -c * grp_max16(m[r]);
+    mc[0] = -c * row_lane0(sa[0].x);
+    mc[1] = -c * row_lane0(sa[0].y);
+    mc[2] = -c * row_lane0(sa[0].z);
+    mc[3] = -c * row_lane0(sa[0].w);
     row_stage_exp<NQ == 1, NQ>(0, sa, c, mc, vis, sel, pw, lsum);
     row_stage_exp<NQ == 1, NQ>(1, sb, c, mc, vis, sel, pw, lsum);
   }
@@ -1467,8 +1477,8 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
 // One (token, group) row with the whole key block in LDS.  kOutQ = out_cols/64
 // is a compile-time count: the row is written by exactly kOutQ 64-column
 // stores (computed quads, then zeros).  A row of nq visible quads runs the
-// straight-line row_fast<nq>; a row whose first-quad reference fails runs
-// the general pipeline against its exact max.
+// straight-line row_fast<nq>; a row whose key-0 reference fails runs the
+// general pipeline against its exact max.
 template <typename OutT, int kOutQ>
 __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Segment& sg,
                                         int32_t lq, const Frag& qf, f16x8 sel) {
