@@ -29,7 +29,6 @@ struct PoolArgs {
   int64_t H, Tq, B, F, NB;
   int32_t block_size, P, local_blocks, init_blocks;
   int64_t n_chunks;  // chunks of 256 outputs per row
-  int64_t n_units;   // (row, chunk) units: H * Tq * n_chunks
 };
 
 template <typename T>
@@ -145,13 +144,14 @@ struct RowCtx {
   int64_t lk, ob, base, lim;
 };
 
-__device__ __forceinline__ RowCtx row_ctx(const PoolArgs& a, int64_t row) {
-  const int64_t t = row % a.Tq;
+__device__ __forceinline__ RowCtx row_ctx(const PoolArgs& a, int64_t row, int64_t t) {
   const int b = find_sequence(a.cu_q, a.B, t);
   RowCtx c{0, 0, row * a.F, 0};
   if (b >= 0) {
     c.lk = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
-    c.ob = (t - a.cu_q[b]) / a.block_size;
+    // 0 <= t - cu_q[b] < 2^31: a 32-bit division (a 64-bit one is a long
+    // emulated sequence)
+    c.ob = static_cast<uint32_t>(t - a.cu_q[b]) / static_cast<uint32_t>(a.block_size);
   }
   // Taps are present below the key length, inside the input, and below the
   // last tap any output window uses (4*NB - 1).
@@ -167,12 +167,24 @@ __device__ __forceinline__ void pool4(const PoolArgs& a, const RowCtx& c, int64_
   const int64_t n0 = chunk * 256 + 4 * lane;
   const int64_t p0 = 4 * n0;
   float v[16];
-  if (kVec && p0 + 15 < c.lim) {
+  // Taps of this lane below the limit.  A lane straddling it still loads
+  // whole vectors when they lie inside the input, and masks the taps past
+  // the limit: only at the input's very end does a lane load tap by tap.
+  const int64_t avail = c.lim - p0;
+  const bool in_alloc = c.base + p0 + 15 < a.numel;
+  if (kVec && avail > 0 && (avail >= 16 || in_alloc)) {
     Vec16<T>::load(a.in, c.base + p0, v);
-  } else {
+    if (avail < 16) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = j < avail ? v[j] : -INFINITY;
+    }
+  } else if (avail > 0) {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       v[j] = (p0 + j < c.lim) ? Elem<T>::load(a.in, c.base + p0 + j) : -INFINITY;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = -INFINITY;
   }
   float prev = __shfl_up(v[15], 1);
   if (lane == 0) {
@@ -206,14 +218,32 @@ __device__ __forceinline__ void store_pooled(const PoolArgs& a, int64_t row, int
   }
 }
 
+// The (token, chunk) unit of a wave: blockIdx.y is the head and the waves of
+// blockIdx.x run over the Tq*n_chunks units of that head (below 2^31, checked
+// by the launcher), so a unit's token needs at most a 32-bit division.
+struct Unit {
+  int64_t row, t, chunk;  // row = h*Tq + t
+  bool ok;
+};
+__device__ __forceinline__ Unit pool_unit(const PoolArgs& a) {
+  const uint32_t v = blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const uint32_t nc = static_cast<uint32_t>(a.n_chunks);
+  const uint32_t t = nc == 1 ? v : v / nc;
+  Unit u;
+  u.t = t;
+  u.chunk = v - t * nc;
+  u.row = static_cast<int64_t>(blockIdx.y) * a.Tq + t;
+  u.ok = t < a.Tq;
+  return u;
+}
+
 template <typename T, bool kVec>
 __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
-  const int64_t u = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (u >= a.n_units) return;  // wave-uniform
+  const Unit un = pool_unit(a);
+  if (!un.ok) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = u / a.n_chunks;  // h*Tq + t
-  const int64_t chunk = u - row * a.n_chunks;
-  const RowCtx c = row_ctx(a, row);
+  const int64_t row = un.row, chunk = un.chunk;
+  const RowCtx c = row_ctx(a, row, un.t);
   float r[4];
   pool4<T, kVec>(a, c, chunk, r);
   store_pooled<T, kVec>(a, row, chunk * 256 + 4 * lane, r);
@@ -242,21 +272,29 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// Wave-wide max / min (wave-uniform results): DPP within each 16-lane row
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
+// then the four rows' results through readlane.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t rows4_u32(uint32_t v, int r) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16 * r));
+}
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), d));
-    v = o > v ? o : v;
-  }
-  return v;
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  return max(max(rows4_u32(v, 0), rows4_u32(v, 1)), max(rows4_u32(v, 2), rows4_u32(v, 3)));
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), d));
-    v = o < v ? o : v;
-  }
-  return v;
+  v = min(v, dpp_u32<0xB1>(v));
+  v = min(v, dpp_u32<0x4E>(v));
+  v = min(v, dpp_u32<0x141>(v));
+  v = min(v, dpp_u32<0x140>(v));
+  return min(min(rows4_u32(v, 0), rows4_u32(v, 1)), min(rows4_u32(v, 2), rows4_u32(v, 3)));
 }
 
 // Lanes below this one whose bit is set in mask.
@@ -268,10 +306,11 @@ __device__ __forceinline__ int32_t lanes_below(uint64_t mask) {
 template <int NCH>
 __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* topk, int32_t K,
                                                            int32_t store) {
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (row >= a.H * a.Tq) return;  // wave-uniform
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  if (t >= a.Tq) return;  // wave-uniform
+  const int64_t row = static_cast<int64_t>(blockIdx.y) * a.Tq + t;  // blockIdx.y: the head
   const int lane = threadIdx.x & (kWave - 1);
-  const RowCtx c = row_ctx(a, row);
+  const RowCtx c = row_ctx(a, row, t);
   const int32_t NB = static_cast<int32_t>(a.NB);
   __shared__ uint32_t short_list[4][kTopkShortList];  // one per wave of the 256-thread block
   // Keys of blocks n = 256*ch + 4*lane + e; 0 (below every real key) past NB.
@@ -302,7 +341,7 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
     // distinct keys lie at or above it).  tau shares every bit above the
     // highest bit where the two differ, so the search starts there.  With
     // one chunk (four keys a lane) the bounds cost more than the steps they
-    // save (measured).
+    // save (measured, with the reductions on ds_bpermute and on DPP alike).
     int top = 31;
     bool searched = false;
     const int32_t n_inf = NCH >= 2 && K <= kWave ? count_ge(kKeyPosInf) : K;
@@ -426,17 +465,15 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
 // General path: any P >= 1 (window of P+1 taps, padding 1); one output per lane.
 template <typename T>
 __global__ __launch_bounds__(256) void maxpool_generic_kernel(PoolArgs a) {
-  const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (wave >= a.n_units) return;
+  const Unit un = pool_unit(a);
+  if (!un.ok) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = wave / a.n_chunks;
-  const int64_t chunk = wave - row * a.n_chunks;
-  const int64_t t = row % a.Tq;
+  const int64_t row = un.row, chunk = un.chunk, t = un.t;
   const int b = find_sequence(a.cu_q, a.B, t);
   int64_t lk = 0, ob = 0;
   if (b >= 0) {
     lk = static_cast<int64_t>(a.cu_k[b + 1] - a.cu_k[b]) + a.cache[b];
-    ob = (t - a.cu_q[b]) / a.block_size;
+    ob = static_cast<uint32_t>(t - a.cu_q[b]) / static_cast<uint32_t>(a.block_size);
   }
   const int64_t base = row * a.F;
   const int64_t lim = lk < (a.numel - base) ? lk : (a.numel - base);
@@ -460,30 +497,37 @@ __global__ __launch_bounds__(256) void maxpool_generic_kernel(PoolArgs a) {
 template <typename T>
 int launch_pool(const PoolArgs& a, hipStream_t s) {
   const int threads = 256;
-  const int64_t blocks = (a.n_units * kWave + threads - 1) / threads;  // generic: one wave per unit
-  if (blocks > INT32_MAX) UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen: too many rows");
+  // One wave per (token, chunk) unit; blockIdx.y is the head.
+  const int64_t units = a.Tq * a.n_chunks;
+  if (units >= (int64_t{1} << 31) || a.H > 65535)
+    UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen: too many rows (H=%lld, Tq=%lld)",
+              (long long)a.H, (long long)a.Tq);
+  const dim3 blocks(static_cast<unsigned>((units + threads / kWave - 1) / (threads / kWave)),
+                    static_cast<unsigned>(a.H));
   if (a.P == 4) {
-    const int64_t blocks4 = blocks;  // one wave per unit
+    const dim3 blocks4 = blocks;
     // Vector loads need 16-byte aligned taps (F a multiple of 16 bytes' worth of
     // elements), vector stores 16/8-byte aligned output runs (NB % 4 == 0).
     const bool vec = (reinterpret_cast<uintptr_t>(a.in) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
                      ((a.F * (int64_t)sizeof(T)) % 16) == 0 && (a.NB % 4) == 0;
     if (vec)
-      hipLaunchKernelGGL((maxpool_p4_kernel<T, true>), dim3((unsigned)blocks4), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((maxpool_p4_kernel<T, true>), blocks4, dim3(threads), 0, s, a);
     else
-      hipLaunchKernelGGL((maxpool_p4_kernel<T, false>), dim3((unsigned)blocks4), dim3(threads), 0, s, a);
+      hipLaunchKernelGGL((maxpool_p4_kernel<T, false>), blocks4, dim3(threads), 0, s, a);
   } else {
-    hipLaunchKernelGGL((maxpool_generic_kernel<T>), dim3((unsigned)blocks), dim3(threads), 0, s, a);
+    hipLaunchKernelGGL((maxpool_generic_kernel<T>), blocks, dim3(threads), 0, s, a);
   }
   return check_launch("max_pooling_1d_varlen");
 }
 
 int launch_topk(const PoolArgs& a, int32_t* topk, int32_t K, int32_t store, hipStream_t s) {
   const int nch = static_cast<int>((a.NB + 255) / 256);
-  const int64_t blocks = (a.H * a.Tq * kWave + 255) / 256;
-  if (blocks > INT32_MAX) UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen_topk: too many rows");
-  const dim3 g(static_cast<unsigned>(blocks)), b(256);
+  // One wave per row: the token on blockIdx.x (four a workgroup), the head on blockIdx.y.
+  if (a.Tq >= (int64_t{1} << 31) || a.H > 65535)
+    UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "max_pooling_1d_varlen_topk: too many rows (H=%lld, Tq=%lld)",
+              (long long)a.H, (long long)a.Tq);
+  const dim3 g(static_cast<unsigned>((a.Tq + 3) / 4), static_cast<unsigned>(a.H)), b(256);
   switch (nch) {
 #define UNUM_TOPK_CASE(N) \
     case N: hipLaunchKernelGGL((maxpool_topk_kernel<N>), g, b, 0, s, a, topk, K, store); break;
@@ -543,7 +587,6 @@ extern "C" int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel
   a.local_blocks = local_blocks;
   a.init_blocks = init_blocks;
   a.n_chunks = (num_blocks + 255) / 256;
-  a.n_units = H * Tq * a.n_chunks;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case UNUM_DTYPE_F32: return launch_pool<float>(a, s);
@@ -605,6 +648,5 @@ extern "C" int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_
   a.local_blocks = local_blocks;
   a.init_blocks = init_blocks;
   a.n_chunks = (num_blocks + 255) / 256;
-  a.n_units = H * Tq * a.n_chunks;
   return launch_topk(a, topk_idx, topk, pooled != nullptr ? 1 : 0, static_cast<hipStream_t>(stream));
 }
