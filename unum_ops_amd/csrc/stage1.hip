@@ -868,9 +868,13 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
       return v < a.out_cols ? v : static_cast<int32_t>(a.out_cols);
     };
     int32_t vis_min = INT32_MAX;
+    // Wave w owns tokens TW*w .. TW*w+TW-1 of the piece: in a piece of fewer
+    // than R tokens the last waves own none and skip their scores (they still
+    // issue every load, barrier and -- dropped -- store, so the waits stay
+    // exact).
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
-      const int64_t i = wave + static_cast<int64_t>(W) * k;
+      const int64_t i = static_cast<int64_t>(TW) * wave + k;
       own[k] = i < n;
       lq[k] = static_cast<int32_t>(sg.t0 + (own[k] ? i : n - 1));
       vis[k] = vis_of(lq[k]);
@@ -885,8 +889,9 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     const int ch_hi = kSplit ? (ch_lo + sp.chunks < nch ? ch_lo + sp.chunks : nch) : nch;
     // Workspace row of token k: the row it is computed for (a repeated
     // token reads the row of the one it repeats).
+    const bool active = own[0];  // wave-uniform
     auto ws_row = [&](int k) -> int64_t {
-      const int64_t i = own[k] ? wave + static_cast<int64_t>(W) * k : n - 1;
+      const int64_t i = own[k] ? static_cast<int64_t>(TW) * wave + k : n - 1;
       return ((static_cast<int64_t>(blockIdx.x) * sp.n_splits) * R + i) * 16;
     };
     Frag qf[TW];
@@ -983,10 +988,10 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 #pragma unroll
         for (int qd = 0; qd < CT / 4; ++qd) {
           f32x4 acc[TW][4];
-          stream_scores<TW>(buf, qd, qf, acc);
+          if (active) stream_scores<TW>(buf, qd, qf, acc);
           const int key0 = kChunkKeys * ch + 64 * qd;  // first key of the quad
           const bool masked = key0 + 64 > vis_min;              // wave-uniform
-          if (pass == 0) {
+          if (pass == 0 && active) {
             if (masked) {
 #pragma unroll
               for (int k = 0; k < TW; ++k)
@@ -1073,39 +1078,41 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             for (int k = 0; k < TW; ++k)
 #pragma unroll
               for (int rr = 0; rr < 4; ++rr) l[k][rr] += le[k][rr];
-          } else {
+          } else if (pass != 0) {
 #pragma unroll
             for (int k = 0; k < TW; ++k) {
-              f32x4 p[4];
-#pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                p[u].x = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].x, c, nb[k][0]));
-                p[u].y = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].y, c, nb[k][1]));
-                p[u].z = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].z, c, nb[k][2]));
-                p[u].w = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].w, c, nb[k][3]));
-              }
-              if (masked) {
+              f32x4 o = {0.f, 0.f, 0.f, 0.f};
+              if (active) {
+                f32x4 p[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                  const bool ok = key0 + 16 * u + (lane & 15) < vis[k];
-                  p[u].x = ok ? p[u].x : 0.f;
-                  p[u].y = ok ? p[u].y : 0.f;
-                  p[u].z = ok ? p[u].z : 0.f;
-                  p[u].w = ok ? p[u].w : 0.f;
+                  p[u].x = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].x, c, nb[k][0]));
+                  p[u].y = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].y, c, nb[k][1]));
+                  p[u].z = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].z, c, nb[k][2]));
+                  p[u].w = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].w, c, nb[k][3]));
                 }
-              }
-              // f16 packs (rounded toward zero: one instruction per pair).
-              uint32_t pk[8];
+                if (masked) {
 #pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                pk[2 * u] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[u].x, p[u].y));
-                pk[2 * u + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[u].z, p[u].w));
+                  for (int u = 0; u < 4; ++u) {
+                    const bool ok = key0 + 16 * u + (lane & 15) < vis[k];
+                    p[u].x = ok ? p[u].x : 0.f;
+                    p[u].y = ok ? p[u].y : 0.f;
+                    p[u].z = ok ? p[u].z : 0.f;
+                    p[u].w = ok ? p[u].w : 0.f;
+                  }
+                }
+                // f16 packs (rounded toward zero: one instruction per pair).
+                uint32_t pk[8];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                  pk[2 * u] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[u].x, p[u].y));
+                  pk[2 * u + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(p[u].z, p[u].w));
+                }
+                const f16x8 b01 = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+                const f16x8 b23 = __builtin_bit_cast(f16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+                o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, o, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, o, 0, 0, 0);
               }
-              const f16x8 b01 = __builtin_bit_cast(f16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
-              const f16x8 b23 = __builtin_bit_cast(f16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
-              f32x4 o = {0.f, 0.f, 0.f, 0.f};
-              o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, o, 0, 0, 0);
-              o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, o, 0, 0, 0);
               buffer_store_out<OutT>(orsrc[k], (key0 + lane) * static_cast<int>(sizeof(OutT)), o.x);
               if constexpr (kPool) pool_quad(pp, prsrc[k], key0, sg.lk, lq[k] >> 6, o.x, carry_out[k]);
             }
