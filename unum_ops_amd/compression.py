@@ -42,10 +42,12 @@ class CompressionPlan:
         self.max_len = int(lk.max()) if self.B > 0 else 0
         self.raw_total = int(cu[-1]) if self.B > 0 else 0
         self.kernel_size, self.stride, self.H, self.D = kernel_size, stride, H, D
-        # Windows per wave: enough waves to fill the GPU, at most eight
-        # windows per lane group (a group re-reads one half-block per run).
+        # Windows per lane group: a group loads and sums each half-block of
+        # its run of windows once, so longer runs load less; about 512 waves
+        # in all measured fastest (8 windows a group on cfg5's 8447 windows,
+        # 16 on 18.7K), at most 16 a group.
         groups = 64 // max(1, H * (D // 8))
-        per_group = max(1, min(8, self.total // (4096 * max(groups, 1))))
+        per_group = max(1, min(16, self.total // (512 * max(groups, 1))))
         self.per_unit = per_group * max(groups, 1)
         units = (lk + self.per_unit - 1) // self.per_unit
         prefix = torch.zeros(self.B + 1, dtype=torch.int64)

@@ -15,9 +15,10 @@
 // Work decomposition: a wave owns a unit of consecutive windows of one
 // sequence; each lane owns one 8-element slice (16 bytes) of one head, a row
 // of the group's lanes covering all heads and dims of a token, and the
-// wave's lane groups split the unit's windows between them.  A lane issues
-// all 32 token loads of a window at once (each raw key is read from HBM
-// once; the half-block two windows share comes the second time from L2).
+// wave's lane groups split the unit's windows between them.  A lane group
+// walks its consecutive windows loading and summing every half-block once
+// (16 token loads at once, the next half-block's while the current one is
+// summed): each raw key is read once.
 #include "common.h"
 
 namespace unum {
@@ -55,21 +56,32 @@ __device__ __forceinline__ void add8(float* acc, i32x4 w) {
   }
 }
 
-// Window j of a lane's slice: the 2*kStride token rows 16j .. are loaded
-// together, then each half-block is summed in token order.
+// Half-block hb of a lane's slice: its kStride token rows, loaded at once.
 template <int kStride>
-__device__ __forceinline__ void window(const __bf16* kb, int64_t k_st, int64_t j, float* h0,
-                                       float* h1) {
-  i32x4 w[2 * kStride];
+__device__ __forceinline__ void half_load(const __bf16* kb, int64_t k_st, int64_t hb, i32x4 (&w)[kStride]) {
 #pragma unroll
-  for (int i = 0; i < 2 * kStride; ++i)
-    w[i] = *reinterpret_cast<const i32x4*>(kb + (j * kStride + i) * k_st);
+  for (int i = 0; i < kStride; ++i) w[i] = *reinterpret_cast<const i32x4*>(kb + (hb * kStride + i) * k_st);
+}
+
+// Their sum, in token order.
+template <int kStride>
+__device__ __forceinline__ void half_sum(const i32x4 (&w)[kStride], float* h) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) h0[e] = h1[e] = 0.f;
+  for (int e = 0; e < 8; ++e) h[e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < kStride; ++i) add8(h0, w[i]);
+  for (int i = 0; i < kStride; ++i) add8(h, w[i]);
+}
+
+// Window j = (half-block j + half-block j+1) / kernel, rounded to bf16.
+__device__ __forceinline__ void store_window(uint16_t* o, const float* h0, const float* h1, float inv) {
+  uint32_t pk[4];
 #pragma unroll
-  for (int i = 0; i < kStride; ++i) add8(h1, w[kStride + i]);
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = f32_to_bf16_bits((h0[2 * e] + h1[2 * e]) * inv);
+    const uint32_t hi = f32_to_bf16_bits((h0[2 * e + 1] + h1[2 * e + 1]) * inv);
+    pk[e] = lo | (hi << 16);
+  }
+  *reinterpret_cast<i32x4*>(o) = i32x4{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
 }
 
 template <int kStride>
@@ -99,20 +111,28 @@ __global__ __launch_bounds__(256) void compress_keys_kernel(CompressArgs a) {
   const int64_t j_lo = (run * groups + grp) * a.per_group;
   int64_t j_hi = j_lo + a.per_group;
   j_hi = j_hi < lk ? j_hi : lk;
+  if (j_lo >= j_hi) return;
   const __bf16* kb = a.k + r0 * a.k_st + h * a.k_sh + d0;
   uint16_t* ob = a.out + (c0 * a.H + h) * a.D + d0;
-  for (int64_t j = j_lo; j < j_hi; ++j) {
-    float h0[8], h1[8];
-    window<kStride>(kb, a.k_st, j, h0, h1);
-    uint32_t pk[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = f32_to_bf16_bits((h0[2 * e] + h1[2 * e]) * a.inv_kernel);
-      const uint32_t hi = f32_to_bf16_bits((h0[2 * e + 1] + h1[2 * e + 1]) * a.inv_kernel);
-      pk[e] = lo | (hi << 16);
-    }
-    *reinterpret_cast<i32x4*>(ob + j * a.H * a.D) =
-        i32x4{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+  const int64_t o_st = static_cast<int64_t>(a.H) * a.D;
+  // Windows j_lo .. j_hi-1 use half-blocks j_lo .. j_hi, each loaded and
+  // summed once; two register buffers alternate, so the next half-block
+  // loads while the current one is summed.
+  i32x4 w0[kStride], w1[kStride];
+  float hp[8], hn[8];
+  half_load<kStride>(kb, a.k_st, j_lo, w0);
+  half_load<kStride>(kb, a.k_st, j_lo + 1, w1);
+  half_sum<kStride>(w0, hp);
+  for (int64_t j = j_lo; j < j_hi; j += 2) {
+    // w1 holds half-block j+1
+    if (j + 2 <= j_hi) half_load<kStride>(kb, a.k_st, j + 2, w0);
+    half_sum<kStride>(w1, hn);
+    store_window(ob + j * o_st, hp, hn, a.inv_kernel);
+    if (j + 1 >= j_hi) break;
+    // w0 holds half-block j+2
+    if (j + 3 <= j_hi) half_load<kStride>(kb, a.k_st, j + 3, w1);
+    half_sum<kStride>(w0, hp);
+    store_window(ob + (j + 1) * o_st, hn, hp, a.inv_kernel);
   }
 }
 
