@@ -709,6 +709,14 @@ constexpr int kStWaves = 8, kStChunkTiles = 8, kStRing = 3;
 // Key splits: 48 KiB of LDS and at most 168 VGPRs, so three workgroups share
 // a CU.
 constexpr int kStSplitWaves = 4, kStSplitTiles = 4, kStSplitRing = 3;
+// Batches of long sequences (at least 16 new tokens each on average) run the
+// key splits with eight waves: pieces of 16 tokens share each K chunk (cfg5
+// measured 7 % faster); short ones keep four (cfg4 measured 20 % slower with
+// eight: half as many pieces, fewer workgroups at once).
+constexpr int kStSplitWavesWide = 8;
+__host__ __device__ inline int split_waves(int64_t Tq, int64_t B) {
+  return Tq >= 16 * B ? kStSplitWavesWide : kStSplitWaves;
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -1856,8 +1864,8 @@ Stage1Path stage1_path(const Stage1Args& a) {
   return mfma ? kPathRowMfma : kPathGeneric;
 }
 
-// Key-split plan of the streaming path: pieces of 8 tokens (four waves of
-// two) times splits of `chunks` 64-key chunks, about six workgroups per CU in
+// Key-split plan of the streaming path: pieces of 2W tokens (W waves of two,
+// W from split_waves) times splits of `chunks` 64-key chunks, about six workgroups per CU in
 // all against the piece bound (measured on decode batches: four left CUs
 // idle, eight and more spent more on combining the splits; pieces of 4
 // tokens measured slower);
@@ -1870,7 +1878,7 @@ struct SplitPlan {
 };
 
 SplitPlan split_plan(int64_t Hkv, int64_t Tq, int64_t B, int64_t out_cols) {
-  constexpr int R = kStSplitWaves * kStTokensPerWave;
+  const int R = split_waves(Tq, B) * kStTokensPerWave;
   constexpr int64_t kChunkKeys = kStSplitTiles * 16;
   SplitPlan p{};
   p.pieces = piece_grid(Hkv, Tq, B, R);
@@ -1934,13 +1942,23 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
     if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes) {
       const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
       const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
-      const dim3 block(kStSplitWaves * kWave);
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 1>),
-                         grid, block, 0, s, a, pp, sp);
-      const int st = check_launch("infllmv2_attn_stage1");
-      if (st != UNUM_OK) return st;
-      hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStSplitWaves, kTW, kStSplitTiles, kStSplitRing, false, 2>),
-                         grid, block, 0, s, a, pp, sp);
+      if (split_waves(a.Tq, a.B) == kStSplitWavesWide) {
+        constexpr int W = kStSplitWavesWide;
+        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 1>),
+                           grid, dim3(W * kWave), 0, s, a, pp, sp);
+        const int st = check_launch("infllmv2_attn_stage1");
+        if (st != UNUM_OK) return st;
+        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 2>),
+                           grid, dim3(W * kWave), 0, s, a, pp, sp);
+      } else {
+        constexpr int W = kStSplitWaves;
+        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 1>),
+                           grid, dim3(W * kWave), 0, s, a, pp, sp);
+        const int st = check_launch("infllmv2_attn_stage1");
+        if (st != UNUM_OK) return st;
+        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 2>),
+                           grid, dim3(W * kWave), 0, s, a, pp, sp);
+      }
     } else {
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, false, 0>),
                          dim3(static_cast<unsigned>(piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW))),
