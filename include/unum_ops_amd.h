@@ -135,7 +135,8 @@ int unum_infllmv2_attn_stage1_maxpool(const void* q, int64_t q_stride_t, int64_t
  * that fall in [0, Lk), Lk = cu_k[b+1]-cu_k[b]+cache_lens[b]; +inf for
  * n < init_blocks or n <= (t-cu_q[b])/block_size <= n+local_blocks; -inf for an
  * empty window.  A tap whose flat address is >= input_numel is treated as
- * absent (the reference reads out of bounds there).
+ * absent (the reference reads out of bounds there).  H <= 65535 and
+ * Tq * ceil(num_blocks / 256) < 2^31 (UNUM_ERR_INVALID_ARGUMENT otherwise).
  */
 int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel, int32_t dtype,
                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
@@ -157,8 +158,9 @@ int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel, int32_t d
  *            num_blocks is -1, and the -1 entries come first.
  *   pooled   optional [H, Tq, num_blocks] fp32 (NULL: not written); when given
  *            it must be 16-byte aligned with num_blocks % 4 == 0.
- * Other arguments as unum_max_pooling_1d_varlen.  num_blocks <= 4096; the
- * input rows must be 16-byte aligned (input aligned, flat_stride % 4 == 0).
+ * Other arguments as unum_max_pooling_1d_varlen.  num_blocks <= 4096,
+ * H <= 65535, Tq < 2^31; the input rows must be 16-byte aligned (input
+ * aligned, flat_stride % 4 == 0).
  */
 int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_numel,
                                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
