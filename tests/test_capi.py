@@ -62,6 +62,12 @@ def test_maxpool_rejects_bad_arguments():
     assert st == _lib.UNUM_ERR_INVALID_ARGUMENT and b"exceeds" in lib.unum_last_error()
     st = lib.unum_max_pooling_1d_varlen(x, 64, 7, x, x, x, x, 2, 8, 1, 4, 2, 64, 16, 1, 1, n)
     assert st == _lib.UNUM_ERR_UNSUPPORTED
+    # more heads than the grid's y dimension holds (the head is blockIdx.y)
+    st = lib.unum_max_pooling_1d_varlen(x, 70000, 0, x, x, x, x, 70000, 1, 1, 1, 1, 64, 16, 1, 1, n)
+    assert st == _lib.UNUM_ERR_INVALID_ARGUMENT and b"too many rows" in lib.unum_last_error()
+    st = lib.unum_max_pooling_1d_varlen_topk(x, 280000, x, x, x, n, x, 70000, 1, 1, 4, 1, 64, 16,
+                                             1, 1, 1, n)
+    assert st == _lib.UNUM_ERR_INVALID_ARGUMENT and b"too many rows" in lib.unum_last_error()
 
 
 def test_stage1_rejects_bad_arguments():
