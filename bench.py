@@ -43,7 +43,7 @@ def parse():
                                        "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
                                        "compress_keys_cfg5", "stage1_maxpool",
                                        "stage1_maxpool_cfg5", "stage1_cfg4", "stage1_decode",
-                                       "copy"],
+                                       "stage1_peaky", "copy"],
                     default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
@@ -139,6 +139,15 @@ def main():
                                     s1g["cu_seqlens_k"], max_seqlen_k=s1g["max_seqlen_k"],
                                     causal=True)
 
+    # cfg3 with its keys times 8 (exact in bf16): peaky scores, as real
+    # attention has, against the nearly flat softmax of mean-pooled keys.
+    k_peaky = s1g["k"] * 8
+
+    def op_stage1_peaky():
+        return infllmv2_attn_stage1(s1g["q"], k_peaky, None, s1g["cu_seqlens_q"],
+                                    s1g["cu_seqlens_k"], max_seqlen_k=s1g["max_seqlen_k"],
+                                    causal=True)
+
     def op_maxpool():
         return max_pooling_1d_varlen(mpg["input"], mpg["cu_seqlens_q"], mpg["cu_seqlens_k"],
                                      mpg["cache_lens"], **mp_kw)
@@ -202,7 +211,7 @@ def main():
              ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5),
              ("compress_keys_cfg5", op_compress_cfg5), ("stage1_maxpool", op_stage1_maxpool),
              ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5), ("stage1_cfg4", op_stage1_cfg4),
-             ("stage1_decode", op_stage1_decode)]
+             ("stage1_decode", op_stage1_decode), ("stage1_peaky", op_stage1_peaky)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -249,6 +258,15 @@ def main():
                                gbs=nbytes / t / 1e9, pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
                                flop=flop, bytes=nbytes, bound="hbm",
                                config="cfg3 4x8192 causal, Hq32/Hkv2/D128, fp32 out [2,32768,512]")
+    if "stage1_peaky" in per_op:
+        flop, nbytes, _ = workloads.stage1_work(s1["cu_seqlens_q"], s1["cu_seqlens_k"], 32, 2,
+                                                128, 512)
+        t = per_op["stage1_peaky"] * 1e-3
+        comps["stage1_peaky"] = dict(us=per_op["stage1_peaky"] * 1e3, tflops=flop / t / 1e12,
+                                     pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                                     gbs=nbytes / t / 1e9, pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                     flop=flop, bytes=nbytes, bound="hbm",
+                                     config="cfg3 with keys x8 (peaky scores), fp32 out [2,32768,512]")
     if "maxpool" in per_op:
         nbytes = workloads.maxpool_bytes(mp["cu_seqlens_q"], mp["cu_seqlens_k"], mp["cache_lens"],
                                          2, 256)

@@ -1196,17 +1196,17 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 // sixteen (which spill).
 //
 // Softmax with one exp per score: the exponentials are taken against each
-// head's score of key 0 (a reference, not the row max; its exponential is 1,
-// so every per-head sum is at least 1) and kept in registers as f16 (rounded
-// toward zero) until the row is done.  The
+// head's max over the row's first 16 keys (a reference, not the row max; the
+// key holding it has exponential 1, so every per-head sum is at least 1) and
+// kept in registers as f16 (rounded toward zero) until the row is done.  The
 // per-head sums and the final head sum both run on the matrix core: every
 // half-quad's f16 pack is multiplied by a 0/1 head selector into a per-head
 // accumulator, and at the end by the heads' 1/sum weights into the output.
 // Every exponential is positive, so a head's sum bounds each of its values:
 // one check per row -- every head's sum at most 2^14 -- proves that no f16
 // value overflowed and that every weight is a normal f16.  A row that fails
-// it (a later key far above key 0) is redone against its exact max, where
-// the sums lie in [1, 512].
+// it (a later key far above the first 16) is redone against its exact max,
+// where the sums lie in [1, 512].
 //
 // Work split: the (group, token) rows of the batch are ordered by sequence,
 // then group, then token in zig-zag order (0, L-1, 1, L-2, ...), and each
@@ -1427,7 +1427,7 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
 }
 
 // Per-head sums of a row from the accumulated selector MFMAs; false when one
-// exceeds 2^14 (the key-0 reference was too low for f16).
+// exceeds 2^14 (the first-tile reference was too low for f16).
 __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
   const float lv[4] = {lsum.x, lsum.y, lsum.z, lsum.w};
   bool bad = false;
@@ -1439,20 +1439,17 @@ __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
   return __builtin_amdgcn_ballot_w64(bad) == 0;
 }
 
-// Lane 16*(l/16) of v, for every lane l: DPP row_newbcast:0 (gfx90a and later).
-__device__ __forceinline__ float row_lane0(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
-}
-
 // A row of exactly NQ visible quads, as one straight-line block: the scores,
 // the exponentials against a per-head reference and their per-head sums,
 // quad by quad (the compiler interleaves one quad's MFMAs with the previous
 // quad's exponentials); only the last quad is masked.  The reference is each
-// head's score of key 0 -- visible in every row with a quad, lane 16g of
-// tile 0 holding it for heads 4g..4g+3 -- so every per-head sum is at least
-// its exponential, 1; a later key more than 14 binary orders above it fails
-// the 2^14 check instead.  Returns false, having stored nothing, when the row
-// needs its exact max.
+// head's max over the visible keys of tile 0 (keys 0..15, one 16-lane
+// reduction per head), so every per-head sum is at least the exponential of
+// that key, 1.  Measured on cfg3 against the 64-key quad max (more VALU per
+// row): 123-126 us against 130-132 on flat scores, 129-133 against 128-130
+// with peaky keys (x8).  Key 0 alone was no faster on flat scores and 70 %
+// slower on peaky ones, where a fifth of the rows fail the 2^14 check below.
+// Returns false, having stored nothing, when the row needs its exact max.
 template <typename OutT, int NQ, int kOutQ>
 __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, float c, f16x8 sel,
                                          OutT* orow) {
@@ -1463,10 +1460,15 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
     f32x4 sa[2], sb[2];
     row_half_mfma(kl, 0, qf, sa);
     row_half_mfma(kl, 1, qf, sb);
-    mc[0] = -c * row_lane0(sa[0].x);
-    mc[1] = -c * row_lane0(sa[0].y);
-    mc[2] = -c * row_lane0(sa[0].z);
-    mc[3] = -c * row_lane0(sa[0].w);
+    {
+      const int lane = threadIdx.x & (kWave - 1);
+      // Keys of tile 0 at or past vis only exist in rows of one quad.
+      const bool ok = NQ > 1 || (lane & 15) < vis;
+      mc[0] = -c * grp_max16(ok ? sa[0].x : -INFINITY);
+      mc[1] = -c * grp_max16(ok ? sa[0].y : -INFINITY);
+      mc[2] = -c * grp_max16(ok ? sa[0].z : -INFINITY);
+      mc[3] = -c * grp_max16(ok ? sa[0].w : -INFINITY);
+    }
     row_stage_exp<NQ == 1, NQ>(0, sa, c, mc, vis, sel, pw, lsum);
     row_stage_exp<NQ == 1, NQ>(1, sb, c, mc, vis, sel, pw, lsum);
   }
@@ -1492,8 +1494,8 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
 // One (token, group) row with the whole key block in LDS.  kOutQ = out_cols/64
 // is a compile-time count: the row is written by exactly kOutQ 64-column
 // stores (computed quads, then zeros).  A row of nq visible quads runs the
-// straight-line row_fast<nq>; a row whose key-0 reference fails runs the
-// general pipeline against its exact max.
+// straight-line row_fast<nq>; a row whose first-tile reference fails runs
+// the general pipeline against its exact max.
 template <typename OutT, int kOutQ>
 __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Segment& sg,
                                         int32_t lq, const Frag& qf, f16x8 sel) {
