@@ -678,13 +678,14 @@ __device__ void zero_orphan_rows(const Stage1Args& a, const Stage1Pool& pp, cons
 // For rows longer than the LDS-resident path holds (Kp > 512: long contexts,
 // decode against a large cache).  A workgroup of W waves owns a piece of up
 // to W*TW consecutive tokens of one (sequence, group); wave w computes the
-// tokens w, w+W, ... (TW of them), so every K fragment read from LDS feeds TW
-// score MFMAs.  K streams through a ring of NB LDS buffers in the fragment
-// order of the resident path, CT*16 keys at a time, loaded by buffer-to-LDS
-// loads NB-1 chunks ahead of the one being computed, with one barrier per
-// chunk.  Whole rows run eight waves; key splits (below) run four with a
-// third of the LDS, so that several workgroups share a CU (measured 40%
-// faster on decode batches; eight waves measured faster on long rows).
+// tokens TW*w .. TW*w+TW-1, so every K fragment read from LDS feeds TW score
+// MFMAs.  K streams through a ring of NB LDS buffers (whole key rows per
+// load, laid out as StreamRead describes), CT*16 keys at a time, loaded by
+// buffer-to-LDS loads NB-1 chunks ahead of the one being computed, with one
+// barrier per chunk.  Whole rows run eight waves; key splits (below) run four
+// or eight with a third of the LDS, so that several workgroups share a CU
+// (measured 40% faster on decode batches; eight waves measured faster on long
+// rows).
 //
 // The reference's two passes, with the VALU work per score kept to an fma, an
 // exp and one more op:
@@ -724,9 +725,8 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 constexpr int kDeadOffset = 0x7ffffff0;  // past every K range (< 2^31): reads zero
 
 // Buffer-to-LDS load of chunk `ch` (keys CT*16*ch ..) of the piece's K block
-// into `buf`, in fragment order: wave w loads the fragments f = w, w+W, ...
-// (16-key tile f/4, 32-column block f%4), each one 1 KiB run of LDS written
-// by one buffer_load ... lds.  Keys past the readable range, and every key of
+// into `buf`: wave w issues the loads f = w, w+W, ... (four whole key rows
+// each), each writing one 1 KiB run of LDS by one buffer_load ... lds.  Keys past the readable range, and every key of
 // a chunk that is not `live` (past the piece), read as zero through the
 // buffer range check, so every chunk issues the same loads.  The loads are
 // issued from inline assembly: the compiler cannot tell the ring's buffers
@@ -738,11 +738,14 @@ __device__ __forceinline__ void stream_dma(__amdgpu_buffer_rsrc_t kr, int64_t k_
   const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
   for (int i = 0; i < CT * 4 / W; ++i) {
+    // Load f of the chunk: whole 256-byte rows of keys 4(f%4) .. 4(f%4)+3 of
+    // tile f/4, lane l taking 16-byte piece (l%16) ^ n of key n = 4(f%4) +
+    // l/16 (n counted within the tile), into units f*64 + l (see StreamRead).
     const int f = wave + i * W;
-    const int jt = f >> 2, cc = f & 3;
-    const int key = CT * 16 * ch + 16 * jt + (lane & 15);
-    const int off = live ? static_cast<int>((static_cast<int64_t>(key) * k_st + 32 * cc + 8 * (lane >> 4)) * 2)
-                         : kDeadOffset;
+    const int n = 4 * (f & 3) + (lane >> 4);
+    const int key = CT * 16 * ch + 16 * (f >> 2) + n;
+    const int piece = (lane & 15) ^ n;
+    const int off = live ? static_cast<int>((static_cast<int64_t>(key) * k_st + 8 * piece) * 2) : kDeadOffset;
     const int m0 = __builtin_amdgcn_readfirstlane(
         static_cast<int>(reinterpret_cast<uintptr_t>((lds_void_ptr)(buf + f * kWave))));
     // M0 holds the LDS destination; the compiler's value of M0 is restored.
@@ -754,6 +757,26 @@ __device__ __forceinline__ void stream_dma(__amdgpu_buffer_rsrc_t kr, int64_t k_
         : "s"(m0), "v"(off), "s"(kr)
         : "memory");
   }
+}
+
+// A chunk's layout in LDS: tile t (16 keys) takes units t*256 .. t*256+255,
+// unit 64*(n/4) + 16*(n%4) + (P ^ n) holding the 16-byte piece P (elements
+// 8P .. 8P+7) of key n of the tile.  Each load above then reads whole key
+// rows (a row of one group is 256 contiguous bytes; the 64-byte pieces of
+// 16 keys a fragment needs measured 2.4x slower to stream), and the MFMA B
+// fragment (tile t, column block cc) -- lane L wants piece 4cc + L/16 of key
+// L%16 -- reads unit t*256 + off[cc]: the 16 lanes of a read group hit 16
+// distinct 16-byte bank groups.
+struct StreamRead {
+  int off[kD / 32];
+};
+__device__ __forceinline__ StreamRead stream_read_offsets() {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = lane & 15;
+  StreamRead r;
+#pragma unroll
+  for (int cc = 0; cc < kD / 32; ++cc) r.off[cc] = 64 * (n >> 2) + 16 * (n & 3) + ((4 * cc + (lane >> 4)) ^ n);
+  return r;
 }
 
 // Wait until at most N of this wave's vector memory operations are pending
@@ -784,24 +807,23 @@ __device__ __forceinline__ void chunk_wait(int k) {
 
 // Scores of quad qd (keys 64*qd .. +63 of the chunk in `buf`) for TW tokens.
 template <int TW>
-__device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const Frag (&qf)[TW],
-                                              f32x4 (&acc)[TW][4]) {
-  const int lane = threadIdx.x & (kWave - 1);
-  int qbase = qd * 16 * kWave + lane;
+__device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const StreamRead& rd,
+                                              const Frag (&qf)[TW], f32x4 (&acc)[TW][4]) {
+  int qbase = qd * 16 * kWave;
   asm volatile("" : "+v"(qbase));
-  const bf16x8* kq = buf + qbase;  // fragment (u, cc) at kq[(4u + cc) * 64]
+  const bf16x8* kq = buf + qbase;  // fragment (tile u, cc) at kq[u * 256 + rd.off[cc]]
   bf16x8 cur[4], nxt[4];
 #pragma unroll
   for (int k = 0; k < TW; ++k)
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[k][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int u = 0; u < 4; ++u) cur[u] = kq[(4 * u) * kWave];
+  for (int u = 0; u < 4; ++u) cur[u] = kq[u * 4 * kWave + rd.off[0]];
 #pragma unroll
   for (int cc = 0; cc < kD / 32; ++cc) {
     if (cc + 1 < kD / 32) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) nxt[u] = kq[(4 * u + cc + 1) * kWave];
+      for (int u = 0; u < 4; ++u) nxt[u] = kq[u * 4 * kWave + rd.off[cc + 1]];
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -857,6 +879,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     wb = f16x8{b0, b0, b0, b0, b1, b1, b1, b1};
   }
   const uint32_t row_bytes = static_cast<uint32_t>(a.out_cols * sizeof(OutT));
+  const StreamRead rd = stream_read_offsets();
 
   const int split = kSplit ? static_cast<int>(blockIdx.y) : 0;
   constexpr int kChunkKeys = CT * 16;
@@ -996,7 +1019,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 #pragma unroll
         for (int qd = 0; qd < CT / 4; ++qd) {
           f32x4 acc[TW][4];
-          if (active) stream_scores<TW>(buf, qd, qf, acc);
+          if (active) stream_scores<TW>(buf, qd, rd, qf, acc);
           const int key0 = kChunkKeys * ch + 64 * qd;  // first key of the quad
           const bool masked = key0 + 64 > vis_min;              // wave-uniform
           if (pass == 0 && active) {
