@@ -103,6 +103,21 @@ def test_block_count_not_multiple_of_four(dev):
     _check(d, dev, 8, return_pooled=True, **_kw(4096, 64 * 13))    # pooled asked: unfused
 
 
+@pytest.mark.parametrize("n_seq", [63, 64, 70])
+def test_many_sequences(n_seq, dev):
+    # A row's sequence is found by ballots over cu_seqlens_q, 64 entries a
+    # step: B + 1 = 64, 65 and 71 entries, with cached keys and 40 tokens past
+    # the last sequence.
+    g = np.random.default_rng(n_seq)
+    q_lens = [int(x) for x in g.integers(120, 200, n_seq)]
+    k_lens = [int(x) for x in g.integers(200, 990, n_seq)]
+    cache = [int(x) for x in g.integers(0, 30, n_seq)]
+    d = workloads.maxpool_inputs(q_lens, F=1024, H=2, seed=20 + n_seq, k_lens=k_lens, cache=cache)
+    d["cu_seqlens_q"][-1] -= 40
+    _check(d, dev, 64, **_kw(16 * 1024, 64 * 256, 2, 1))
+    _check(d, dev, 64, return_pooled=False, **_kw(16 * 1024, 64 * 256, 2, 1))
+
+
 def test_tokens_outside_sequences(dev):
     d = workloads.maxpool_inputs([50, 30], F=512, H=2, seed=9)
     d["cu_seqlens_q"] = torch.tensor([0, 20, 60], dtype=torch.int32)  # tokens 60..79 orphan

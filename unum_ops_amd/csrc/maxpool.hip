@@ -144,6 +144,13 @@ struct RowCtx {
   int64_t lk, ob, base, lim;
 };
 
+// Taps are present below the key length, inside the input, and below the
+// last tap any output window uses (4*NB - 1).
+__device__ __forceinline__ void set_tap_limit(const PoolArgs& a, RowCtx& c) {
+  const int64_t lim = c.lk < (a.numel - c.base) ? c.lk : (a.numel - c.base);
+  c.lim = lim < 4 * a.NB ? lim : 4 * a.NB;
+}
+
 __device__ __forceinline__ RowCtx row_ctx(const PoolArgs& a, int64_t row, int64_t t) {
   const int b = find_sequence(a.cu_q, a.B, t);
   RowCtx c{0, 0, row * a.F, 0};
@@ -153,31 +160,32 @@ __device__ __forceinline__ RowCtx row_ctx(const PoolArgs& a, int64_t row, int64_
     // emulated sequence)
     c.ob = static_cast<uint32_t>(t - a.cu_q[b]) / static_cast<uint32_t>(a.block_size);
   }
-  // Taps are present below the key length, inside the input, and below the
-  // last tap any output window uses (4*NB - 1).
-  int64_t lim = c.lk < (a.numel - c.base) ? c.lk : (a.numel - c.base);
-  c.lim = lim < 4 * a.NB ? lim : 4 * a.NB;
+  set_tap_limit(a, c);
   return c;
 }
 
-// Pooled outputs n0..n0+3 (n0 = 256*chunk + 4*lane) of a row.
+// The taps of one lane: v = taps 4*n0 .. 4*n0+15, and below = tap 4*n0-1
+// (loaded by lane 0 only; the other lanes take it from the lane below).
+struct Taps {
+  float v[16];
+  float below;
+};
+
+// Issue the loads of a lane's taps for outputs n0..n0+3 (n0 = 256*chunk + 4*lane).
 template <typename T, bool kVec>
-__device__ __forceinline__ void pool4(const PoolArgs& a, const RowCtx& c, int64_t chunk, float* r) {
+__device__ __forceinline__ void load_taps(const PoolArgs& a, const RowCtx& c, int64_t chunk, Taps& tp) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t n0 = chunk * 256 + 4 * lane;
   const int64_t p0 = 4 * n0;
-  float v[16];
+  float* v = tp.v;
   // Taps of this lane below the limit.  A lane straddling it still loads
-  // whole vectors when they lie inside the input, and masks the taps past
-  // the limit: only at the input's very end does a lane load tap by tap.
+  // whole vectors when they lie inside the input (pool_taps masks the taps
+  // past the limit, so nothing here waits for the loads): only at the
+  // input's very end does a lane load tap by tap.
   const int64_t avail = c.lim - p0;
   const bool in_alloc = c.base + p0 + 15 < a.numel;
   if (kVec && avail > 0 && (avail >= 16 || in_alloc)) {
     Vec16<T>::load(a.in, c.base + p0, v);
-    if (avail < 16) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = j < avail ? v[j] : -INFINITY;
-    }
   } else if (avail > 0) {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
@@ -186,11 +194,28 @@ __device__ __forceinline__ void pool4(const PoolArgs& a, const RowCtx& c, int64_
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = -INFINITY;
   }
-  float prev = __shfl_up(v[15], 1);
+  tp.below = -INFINITY;
   if (lane == 0) {
     const int64_t pe = p0 - 1;
-    prev = (pe >= 0 && pe < c.lim) ? Elem<T>::load(a.in, c.base + pe) : -INFINITY;
+    if (pe >= 0 && pe < c.lim) tp.below = Elem<T>::load(a.in, c.base + pe);
   }
+}
+
+// Pooled outputs n0..n0+3 of a row from the lane's taps.
+__device__ __forceinline__ void pool_taps(const PoolArgs& a, const RowCtx& c, int64_t chunk,
+                                          const Taps& tp, float* r) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t n0 = chunk * 256 + 4 * lane;
+  const int64_t avail = c.lim - 4 * n0;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = tp.v[j];
+  if (avail < 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = j < avail ? v[j] : -INFINITY;
+  }
+  float prev = __shfl_up(v[15], 1);
+  if (lane == 0) prev = tp.below;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t n = n0 + e;
@@ -203,6 +228,14 @@ __device__ __forceinline__ void pool4(const PoolArgs& a, const RowCtx& c, int64_
     const bool force = n < a.init_blocks || (c.ob >= n && c.ob <= n + a.local_blocks);
     r[e] = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
   }
+}
+
+// Pooled outputs n0..n0+3 (n0 = 256*chunk + 4*lane) of a row.
+template <typename T, bool kVec>
+__device__ __forceinline__ void pool4(const PoolArgs& a, const RowCtx& c, int64_t chunk, float* r) {
+  Taps tp;
+  load_taps<T, kVec>(a, c, chunk, tp);
+  pool_taps(a, c, chunk, tp, r);
 }
 
 template <typename T, bool kVec>
@@ -303,26 +336,13 @@ __device__ __forceinline__ int32_t lanes_below(uint64_t mask) {
                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
 }
 
+// The top K of a row's keys (blocks n = 256*ch + 4*lane + e; key 0, below
+// every real key, past NB) into orow.  `list` is the wave's short list in LDS
+// (kTopkShortList keys; unused with one chunk).
 template <int NCH>
-__global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* topk, int32_t K,
-                                                           int32_t store) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
-  if (t >= a.Tq) return;  // wave-uniform
-  const int64_t row = static_cast<int64_t>(blockIdx.y) * a.Tq + t;  // blockIdx.y: the head
+__device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32_t NB, int32_t K,
+                                            int32_t* orow, uint32_t* list) {
   const int lane = threadIdx.x & (kWave - 1);
-  const RowCtx c = row_ctx(a, row, t);
-  const int32_t NB = static_cast<int32_t>(a.NB);
-  __shared__ uint32_t short_list[4][kTopkShortList];  // one per wave of the 256-thread block
-  // Keys of blocks n = 256*ch + 4*lane + e; 0 (below every real key) past NB.
-  uint32_t key[NCH][4];
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) {
-    float r[4];
-    pool4<float, true>(a, c, ch, r);
-    if (store) store_pooled<float, true>(a, row, ch * 256 + 4 * lane, r);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) key[ch][e] = (256 * ch + 4 * lane + e < NB) ? order_key(r[e]) : 0u;
-  }
   auto count_ge = [&](uint32_t cand) -> int32_t {
     int32_t n = 0;
 #pragma unroll
@@ -381,7 +401,6 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
         }
         const int32_t total = __builtin_amdgcn_readfirstlane(__shfl(incl, kWave - 1));
         if (total <= kTopkShortList) {
-          uint32_t* list = short_list[threadIdx.x >> 6];
           int32_t pos = incl - mine;
 #pragma unroll
           for (int ch = 0; ch < NCH; ++ch)
@@ -420,7 +439,6 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   } else {
     neg = count_ge(kKeyNegInf) - count_ge(kKeyNegInf + 1);
   }
-  int32_t* orow = topk + row * K;
   int32_t lead = (NB < K ? K - NB : 0) + neg;  // -1 slots, first
   lead = lead < K ? lead : K;
   for (int32_t j = lane; j < lead; j += kWave) orow[j] = -1;
@@ -460,6 +478,28 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
       eq_seen += __popcll(m_eq[e]);
     }
   }
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* topk, int32_t K,
+                                                           int32_t store) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  if (t >= a.Tq) return;  // wave-uniform
+  const int64_t row = static_cast<int64_t>(blockIdx.y) * a.Tq + t;  // blockIdx.y: the head
+  const int lane = threadIdx.x & (kWave - 1);
+  const RowCtx c = row_ctx(a, row, t);
+  const int32_t NB = static_cast<int32_t>(a.NB);
+  __shared__ uint32_t short_list[4][kTopkShortList];  // one per wave of the 256-thread block
+  uint32_t key[NCH][4];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    float r[4];
+    pool4<float, true>(a, c, ch, r);
+    if (store) store_pooled<float, true>(a, row, ch * 256 + 4 * lane, r);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[ch][e] = (256 * ch + 4 * lane + e < NB) ? order_key(r[e]) : 0u;
+  }
+  topk_select<NCH>(key, NB, K, topk + row * K, short_list[threadIdx.x >> 6]);
 }
 
 // General path: any P >= 1 (window of P+1 taps, padding 1); one output per lane.

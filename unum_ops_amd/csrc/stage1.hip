@@ -1859,19 +1859,6 @@ __global__ __launch_bounds__(kDecWaves* kWave) void stage1_decode_kernel(Stage1A
     store_out<OutT>(orow + j, 0.f);
 }
 
-int num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 enum Stage1Path { kPathLds, kPathStream, kPathRowMfma, kPathGeneric };
 
 template <typename OutT>
