@@ -70,3 +70,12 @@ def test_non_causal_and_orphans(dev):
     d["q"] = q
     d["cu_seqlens_q"] = d["cu_seqlens_q"] + 5
     _check(d, dev, 3000, causal=False)
+
+
+@pytest.mark.parametrize("q_len", [2500, 9000])
+def test_prefill_rows_see_fewer_keys_than_the_pool(q_len, dev):
+    # A prefill over 561 keys (the fused kernel): early tokens see few keys,
+    # so blocks past the columns their piece computes lie over zero scores
+    # below the key count and pool to 0, not -inf.
+    d = workloads.stage1_inputs([q_len], [9000], seed=34)
+    _check(d, dev, 9000)

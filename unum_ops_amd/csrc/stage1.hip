@@ -181,15 +181,20 @@ __device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_r
   carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), kWave - 1));
 }
 
-// Pooled blocks past the computed columns (first = the first such block):
-// only the first can still hold a tap (the last column, via `carry`).
+// Pooled blocks past the computed columns (first = the first such block,
+// 4*first the first column not computed): those columns hold zero scores
+// below lk (keys the row does not see), so a block with a tap there pools to
+// at least 0; the first block's tap 4*first-1 is the last computed column,
+// `carry` (-inf at or past lk).  A block with no tap below lk is -inf.
 __device__ __forceinline__ void pool_tail(const Stage1Pool& a, __amdgpu_buffer_rsrc_t prs,
-                                          int32_t first, int32_t ob, float carry) {
+                                          int32_t first, int32_t lk, int32_t ob, float carry) {
   const int lane = threadIdx.x & (kWave - 1);
   for (int64_t n = first + lane; n < a.nb; n += kWave) {
     const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
-    const float v = force ? INFINITY : (n == first ? carry : -INFINITY);
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), prs, static_cast<int>(n * 4), 0, kStoreNT);
+    const bool zero_tap = n == first ? 4 * n < lk : 4 * n - 1 < lk;
+    const float v = fmaxf(n == first ? carry : -INFINITY, zero_tap ? 0.f : -INFINITY);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(force ? INFINITY : v), prs,
+                                          static_cast<int>(n * 4), 0, kStoreNT);
   }
 }
 
@@ -197,7 +202,7 @@ __device__ __forceinline__ void pool_tail(const Stage1Pool& a, __amdgpu_buffer_r
 
 // Pooled row of a token outside every sequence: no taps, block of the token 0.
 __device__ __forceinline__ void orphan_pool_row(const Stage1Pool& p, int64_t row) {
-  pool_tail(p, make_rsrc(p.pooled + row * p.nb, static_cast<uint32_t>(p.nb * 4)), 0, 0, -INFINITY);
+  pool_tail(p, make_rsrc(p.pooled + row * p.nb, static_cast<uint32_t>(p.nb * 4)), 0, 0, 0, -INFINITY);
 }
 
 // ---------------------------------------------------------------- MFMA path
@@ -1196,7 +1201,8 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
         if constexpr (kPool) {
           // The last streamed column's tap is carried only when a chunk ran.
           pool_tail(pp, make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)),
-                    static_cast<int32_t>(done / 4), lq[k] >> 6, nch > 0 ? carry_out[k] : -INFINITY);
+                    static_cast<int32_t>(done / 4), sg.lk, lq[k] >> 6,
+                    nch > 0 ? carry_out[k] : -INFINITY);
         }
       }
     }
