@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define UNUM_ABI_VERSION 1
+#define UNUM_ABI_VERSION 2
 
 enum unum_status {
   UNUM_OK = 0,
@@ -107,6 +107,10 @@ int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t 
  *
  *   scores  optional fp32 [Hkv, Tq, out_cols] (NULL: not written)
  *   pooled  fp32 [Hkv, Tq, num_blocks]
+ *   workspace / workspace_bytes  as unum_infllmv2_attn_stage1 (size from
+ *          unum_infllmv2_attn_stage1_workspace_size): with it, rows over 512
+ *          keys run the key-split kernels, pooling in their second pass;
+ *          NULL runs whole rows.
  * Other arguments as unum_infllmv2_attn_stage1 and unum_max_pooling_1d_varlen.
  * Only the MFMA paths (G = 16, D = 128, 16-byte aligned q/k, scale > 0) are
  * fused; other shapes return UNUM_ERR_UNSUPPORTED.
@@ -118,7 +122,8 @@ int unum_infllmv2_attn_stage1_maxpool(const void* q, int64_t q_stride_t, int64_t
                                       int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
                                       int64_t max_seqlen_k, int64_t out_cols, float scale,
                                       int32_t causal, int64_t num_blocks, int32_t local_blocks,
-                                      int32_t init_blocks, void* stream);
+                                      int32_t init_blocks, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
 
 /*
  * Varlen 1-D max-pool of compressed-block scores, replacing

@@ -23,7 +23,7 @@ UNUM_DTYPE_F32 = 0
 UNUM_DTYPE_BF16 = 1
 UNUM_DTYPE_F16 = 2
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Every symbol declared in include/unum_ops_amd.h with (restype, argtypes).
 _p = ctypes.c_void_p
@@ -55,6 +55,7 @@ SIGNATURES = {
         _i64, _i64,                # max_seqlen_k, out_cols
         ctypes.c_float, _i32,      # scale, causal
         _i64, _i32, _i32,          # num_blocks, local_blocks, init_blocks
+        _p, _i64,                  # workspace, workspace_bytes
         _p,                        # stream
     ]),
     "unum_max_pooling_1d_varlen": (ctypes.c_int, [

@@ -163,10 +163,10 @@ __device__ __forceinline__ void buffer_store_out(__amdgpu_buffer_rsrc_t r, int o
 // (the -1 tap is the previous quad's last key, `carry`); +inf when forced
 // (n < init_blocks or n <= ob <= n + local_blocks), -inf when no tap is
 // present -- max_pooling_1d_varlen with block 64 / stride 16.  Lanes 4i store
-// block i; `carry` becomes this quad's last tap.
+// block i (nothing is stored when `drop`); `carry` becomes this quad's last tap.
 __device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_rsrc_t prs,
                                           int32_t key0, int32_t lk, int32_t ob, float o,
-                                          float& carry) {
+                                          float& carry, bool drop) {
   const int lane = threadIdx.x & (kWave - 1);
   const float x = key0 + lane < lk ? o : -INFINITY;
   float m = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
@@ -177,7 +177,7 @@ __device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_r
   const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
   const float blk = force ? INFINITY : fmaxf(m, left);
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(blk), prs,
-                                        (lane & 3) == 0 ? n * 4 : kDropOffset, 0, kStoreNT);
+                                        (lane & 3) == 0 && !drop ? n * 4 : kDropOffset, 0, kStoreNT);
   carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), kWave - 1));
 }
 
@@ -848,7 +848,10 @@ __device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const S
 // one split (blockIdx.y) and writes each (row, head)'s log2-sum-exp of the
 // split, c*max + log2(sum), to `ws`; kSplit == 2 combines a row's splits into
 // the bias and runs the second pass over its split, writing that split's
-// columns.  The two launches are the reference's two passes.
+// columns.  The two launches are the reference's two passes.  With the pool
+// fused (second pass only), a split's first block takes its -1 tap from the
+// previous split's last column: the split first computes the chunk before
+// its own, storing nothing, to carry that column in.
 struct Stage1Split {
   float* ws;        // [pieces][n_splits][16 rows][16 heads]
   int32_t chunks;   // 256-key chunks per split
@@ -858,7 +861,7 @@ struct Stage1Split {
 template <typename OutT, int W, int TW, int CT, int NB, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
                                                                  Stage1Split sp) {
-  static_assert(!(kPool && kSplit), "the fused pool runs on whole rows");
+  static_assert(!(kPool && kSplit == 1), "the first pass writes no scores to pool");
   static_assert((CT * 4) % W == 0, "every wave loads the same number of K fragments");
   static_assert(NB >= 2, "a ring of at least two chunks");
   __shared__ bf16x8 kbuf[NB][CT * 4 * kWave];
@@ -923,6 +926,9 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     // Chunks of this launch: all of them, or those of this key split.
     const int ch_lo = kSplit ? (split * sp.chunks < nch ? split * sp.chunks : nch) : 0;
     const int ch_hi = kSplit ? (ch_lo + sp.chunks < nch ? ch_lo + sp.chunks : nch) : nch;
+    // The first chunk streamed: with the pool, a later split starts one
+    // chunk early to carry in the previous split's last column.
+    const int ch_first = kPool && kSplit == 2 && ch_lo > 0 && ch_hi > ch_lo ? ch_lo - 1 : ch_lo;
     // Workspace row of token k: the row it is computed for (a repeated
     // token reads the row of the one it repeats).
     const bool active = own[0];  // wave-uniform
@@ -970,7 +976,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
       __syncthreads();  // the previous user of kbuf is done
 #pragma unroll
       for (int i = 0; i < kAhead; ++i)
-        stream_dma<W, CT>(kr, a.k_st, ch_lo + i, ch_lo + i < ch_hi, kbuf[i], wave);
+        stream_dma<W, CT>(kr, a.k_st, ch_first + i, ch_first + i < ch_hi, kbuf[i], wave);
       if constexpr (kSplit == 2) {
         // Combine the splits' log2-sum-exps of each (row, head): lane group g
         // reads heads 4g..4g+3 of the splits that hold visible keys.
@@ -1012,8 +1018,9 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 #pragma unroll
       for (int k = 0; k < TW; ++k)
         asm volatile("" : : "v"(qf[k].v[0]), "v"(qf[k].v[1]), "v"(qf[k].v[2]), "v"(qf[k].v[3]));
-      for (int ch = ch_lo; ch < ch_hi; ++ch) {
-        const int kc = ch - ch_lo;
+      for (int ch = ch_first; ch < ch_hi; ++ch) {
+        const int kc = ch - ch_first;
+        const bool carry_only = ch < ch_lo;  // the pool's carry chunk: nothing stored
         if (pass == 0)
           chunk_wait<(kAhead - 1) * kLoads, 0, kAhead>(kc);
         else
@@ -1149,8 +1156,11 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
                 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, b01, o, 0, 0, 0);
                 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, b23, o, 0, 0, 0);
               }
-              buffer_store_out<OutT>(orsrc[k], (key0 + lane) * static_cast<int>(sizeof(OutT)), o.x);
-              if constexpr (kPool) pool_quad(pp, prsrc[k], key0, sg.lk, lq[k] >> 6, o.x, carry_out[k]);
+              buffer_store_out<OutT>(orsrc[k],
+                                     carry_only ? kDropOffset : (key0 + lane) * static_cast<int>(sizeof(OutT)),
+                                     o.x);
+              if constexpr (kPool)
+                pool_quad(pp, prsrc[k], key0, sg.lk, lq[k] >> 6, o.x, carry_out[k], carry_only);
             }
           }
         }
@@ -1199,10 +1209,13 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
         if ((!kPool || pp.write_scores) && done < end)
           zero_row_vec<OutT>(static_cast<OutT*>(a.out) + row * a.out_cols, done, end);
         if constexpr (kPool) {
-          // The last streamed column's tap is carried only when a chunk ran.
-          pool_tail(pp, make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)),
-                    static_cast<int32_t>(done / 4), sg.lk, lq[k] >> 6,
-                    nch > 0 ? carry_out[k] : -INFINITY);
+          // Blocks past the computed columns belong to the split whose chunks
+          // end them (the first split when no chunk runs); the last computed
+          // column's tap is carried only when a chunk ran.
+          const bool tail_here = ch_hi > ch_lo ? ch_hi == nch : split == 0;
+          if (tail_here)
+            pool_tail(pp, make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)),
+                      nch * kChunkKeys / 4, sg.lk, lq[k] >> 6, nch > 0 ? carry_out[k] : -INFINITY);
         }
       }
     }
@@ -1911,6 +1924,35 @@ SplitPlan split_plan(int64_t Hkv, int64_t Tq, int64_t B, int64_t out_cols) {
   return p;
 }
 
+// The two key-split launches (per-split sums, then the scores -- and with
+// kPool the pooled blocks -- of each split).
+template <typename OutT, bool kPool>
+int launch_split(const Stage1Args& a, const Stage1Pool& pp, const SplitPlan& plan, void* ws,
+                 hipStream_t s) {
+  constexpr int kTW = kStTokensPerWave;
+  const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
+  const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
+  const char* op = kPool ? "infllmv2_attn_stage1_maxpool" : "infllmv2_attn_stage1";
+  if (split_waves(a.Tq, a.B) == kStSplitWavesWide) {
+    constexpr int W = kStSplitWavesWide;
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 1>),
+                       grid, dim3(W * kWave), 0, s, a, pp, sp);
+    const int st = check_launch(op);
+    if (st != UNUM_OK) return st;
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, kPool, 2>),
+                       grid, dim3(W * kWave), 0, s, a, pp, sp);
+  } else {
+    constexpr int W = kStSplitWaves;
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 1>),
+                       grid, dim3(W * kWave), 0, s, a, pp, sp);
+    const int st = check_launch(op);
+    if (st != UNUM_OK) return st;
+    hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, kPool, 2>),
+                       grid, dim3(W * kWave), 0, s, a, pp, sp);
+  }
+  return check_launch(op);
+}
+
 template <typename OutT, bool kPool>
 int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t ws_bytes,
                   hipStream_t s) {
@@ -1928,6 +1970,10 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
     UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "infllmv2_attn_stage1: %lld tokens and %lld sequences are too many",
               (long long)a.Tq, (long long)a.B);
   if constexpr (kPool) {
+    // Key splits when the caller gave the workspace they need, else whole rows.
+    const SplitPlan plan = split_plan(a.Hkv, a.Tq, a.B, a.out_cols);
+    if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes)
+      return launch_split<OutT, true>(a, pp, plan, ws, s);
     constexpr int kTW = kStTokensPerWave;
     const int64_t grid = piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW);
     hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, true, 0>),
@@ -1958,25 +2004,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
     constexpr int kTW = kStTokensPerWave;
     const SplitPlan plan = split_plan(a.Hkv, a.Tq, a.B, a.out_cols);
     if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes) {
-      const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
-      const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
-      if (split_waves(a.Tq, a.B) == kStSplitWavesWide) {
-        constexpr int W = kStSplitWavesWide;
-        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 1>),
-                           grid, dim3(W * kWave), 0, s, a, pp, sp);
-        const int st = check_launch("infllmv2_attn_stage1");
-        if (st != UNUM_OK) return st;
-        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 2>),
-                           grid, dim3(W * kWave), 0, s, a, pp, sp);
-      } else {
-        constexpr int W = kStSplitWaves;
-        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 1>),
-                           grid, dim3(W * kWave), 0, s, a, pp, sp);
-        const int st = check_launch("infllmv2_attn_stage1");
-        if (st != UNUM_OK) return st;
-        hipLaunchKernelGGL((stage1_stream_kernel<OutT, W, kTW, kStSplitTiles, kStSplitRing, false, 2>),
-                           grid, dim3(W * kWave), 0, s, a, pp, sp);
-      }
+      return launch_split<OutT, false>(a, pp, plan, ws, s);
     } else {
       hipLaunchKernelGGL((stage1_stream_kernel<OutT, kStWaves, kTW, kStChunkTiles, kStRing, false, 0>),
                          dim3(static_cast<unsigned>(piece_grid(a.Hkv, a.Tq, a.B, kStWaves * kTW))),
@@ -2090,7 +2118,8 @@ extern "C" int unum_infllmv2_attn_stage1_maxpool(
     int64_t k_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, void* scores,
     float* pooled, int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
     int64_t max_seqlen_k, int64_t out_cols, float scale, int32_t causal, int64_t num_blocks,
-    int32_t local_blocks, int32_t init_blocks, void* stream) {
+    int32_t local_blocks, int32_t init_blocks, void* workspace, int64_t workspace_bytes,
+    void* stream) {
   using namespace unum;
   clear_error();
   const char* op = "infllmv2_attn_stage1_maxpool";
@@ -2111,5 +2140,6 @@ extern "C" int unum_infllmv2_attn_stage1_maxpool(
   pp.init_blocks = init_blocks;
   pp.local_blocks = local_blocks;
   pp.write_scores = scores != nullptr;
-  return launch_stage1<float, true>(a, pp, nullptr, 0, static_cast<hipStream_t>(stream));
+  return launch_stage1<float, true>(a, pp, workspace, workspace_bytes,
+                                    static_cast<hipStream_t>(stream));
 }

@@ -218,12 +218,17 @@ def infllmv2_attn_stage1_maxpool(q, k, cu_seqlens_q, cu_seqlens_k, max_context_l
         return (pooled, scores) if return_scores else pooled
     lib = _lib.load()
     with torch.cuda.device(dev):
+        # The key-split workspace of stage 1: rows over 512 keys then pool in
+        # the split kernels' second pass.
+        ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(
+            batch, total_q, n_heads, n_kv_heads, head_dim, max_seqlen_k)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
         st = lib.unum_infllmv2_attn_stage1_maxpool(
             _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
             _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(scores), _lib.ptr(pooled),
             batch, total_q, total_k, n_heads, n_kv_heads, head_dim, max_seqlen_k, cols,
             float(softmax_scale), 1 if causal else 0, nb, int(local_blocks), int(init_blocks),
-            _lib.stream_ptr(dev))
+            _lib.ptr(ws), ws_bytes, _lib.stream_ptr(dev))
     if st == _lib.UNUM_ERR_UNSUPPORTED:
         # a layout off the MFMA paths (e.g. unaligned q/k): the two ops take it
         return _unfused(q, k, cu_q, cu_k, max_seqlen_k, softmax_scale, causal, max_context_len,
