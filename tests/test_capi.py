@@ -86,6 +86,22 @@ def test_stage1_rejects_bad_arguments():
     assert lib.unum_infllmv2_attn_stage1_workspace_size(4, 32768, 32, 2, 128, 511) >= 0
 
 
+def test_stage1_maxpool_rejects_bad_arguments():
+    lib = _lib.load()
+    n = _null()
+    # q, strides, k, strides, cu_q, cu_k, scores, pooled, B, Tq, Tk, Hq, Hkv, D,
+    # max_seqlen_k, out_cols, scale, causal, num_blocks, local, init, workspace, bytes, stream
+    st = lib.unum_infllmv2_attn_stage1_maxpool(n, 1, 1, n, 1, 1, n, n, n, n, 1, 4, 4, 32, 2, 128,
+                                               600, 640, 0.1, 1, -1, 1, 1, n, 0, n)
+    assert st == _lib.UNUM_ERR_INVALID_ARGUMENT and b"num_blocks" in lib.unum_last_error()
+    st = lib.unum_infllmv2_attn_stage1_maxpool(n, 1, 1, n, 1, 1, n, n, n, n, 1, 4, 4, 32, 2, 128,
+                                               700, 640, 0.1, 1, 16, 1, 1, n, 0, n)
+    assert st == _lib.UNUM_ERR_INVALID_ARGUMENT and b"max_seqlen_k" in lib.unum_last_error()
+    # nothing to do: success without touching any pointer
+    assert lib.unum_infllmv2_attn_stage1_maxpool(n, 1, 1, n, 1, 1, n, n, n, n, 1, 0, 4, 32, 2,
+                                                 128, 600, 640, 0.1, 1, 16, 1, 1, n, 0, n) == 0
+
+
 def test_check_maps_status_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.UNUM_ERR_INVALID_ARGUMENT, "op")
