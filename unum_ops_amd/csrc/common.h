@@ -39,6 +39,13 @@ inline int check_launch(const char* what) {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
+// Lane i takes v from lane i-1 and lane 0 takes `fill`: a DPP wave_shr:1
+// move (one VALU instruction, no LDS round trip as for a shuffle).
+__device__ __forceinline__ float wave_shr1(float v, float fill) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), 0x138,
+                                                    0xF, 0xF, false));
+}
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 inline int num_cus() {
   static int cached[64] = {0};

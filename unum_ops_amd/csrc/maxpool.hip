@@ -214,8 +214,7 @@ __device__ __forceinline__ void pool_taps(const PoolArgs& a, const RowCtx& c, in
 #pragma unroll
     for (int j = 0; j < 16; ++j) v[j] = j < avail ? v[j] : -INFINITY;
   }
-  float prev = __shfl_up(v[15], 1);
-  if (lane == 0) prev = tp.below;
+  const float prev = wave_shr1(v[15], tp.below);  // tap 4*n0-1
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t n = n0 + e;

@@ -171,8 +171,7 @@ __device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_r
   const float x = key0 + lane < lk ? o : -INFINITY;
   float m = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
   m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
-  float left = __shfl_up(x, 1);
-  left = lane == 0 ? carry : left;
+  const float left = wave_shr1(x, carry);
   const int32_t n = (key0 >> 2) + (lane >> 2);
   const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
   const float blk = force ? INFINITY : fmaxf(m, left);
