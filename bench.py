@@ -57,7 +57,7 @@ def log(msg):
 def build_inputs(dev):
     import torch
 
-    from unum_ops_amd import workloads
+    from tests import workloads
     from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
     from unum_ops_amd.pipeline import topk_blocks
 
@@ -118,7 +118,7 @@ def main():
 
     import torch
 
-    from unum_ops_amd import workloads
+    from tests import workloads
     from unum_ops_amd.compression import CompressionPlan, compress_keys
     from unum_ops_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_maxpool,
                                         max_pooling_1d_varlen)
@@ -431,7 +431,7 @@ def cpu_baseline(s1):
     import torch
 
     from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
-    from unum_ops_amd import workloads
+    from tests import workloads
 
     torch.set_num_threads(os.cpu_count() or 1)
     flop, _, _ = workloads.stage1_work(s1["cu_seqlens_q"], s1["cu_seqlens_k"], 32, 2, 128, 512)

@@ -68,10 +68,21 @@ int unum_abi_version(void);
  * over the visible keys j < vis(t) (causal rule of the reference, truncating
  * division), 0 for vis <= j < out_cols, and 0 for the whole row when
  * vis == 0 or the sequence has no keys.  Every element of `out` is written
- * when cu_seqlens_q is non-decreasing within [0, Tq]; keys of a sequence at
- * j >= out_cols are not (the reference writes past the row there).  The rows
- * of a sequence reaching outside [0, Tq) (malformed cu_seqlens_q) are left
+ * when cu_seqlens_q is non-decreasing within [0, Tq].  The rows of a
+ * sequence reaching outside [0, Tq) (malformed cu_seqlens_q) are left
  * unwritten, never indexed.
+ *
+ * Inputs outside the reference's contract (where it stores past the row or
+ * reads outside k):
+ *   - a sequence with more keys than out_cols (max_seqlen_k below its real
+ *     length): vis is computed from the real key count, then capped at
+ *     out_cols; the row is the softmax over the keys it keeps (the dropped
+ *     keys are in no denominator), so it still sums to G;
+ *   - key ranges of cu_seqlens_k outside [0, Tk): keys outside k read as
+ *     zero; no load leaves k.
+ * q and k must be finite: the reference maps a NaN score row to 0
+ * (infllmv2_attn_stage1_triton_v2.py:227); this library is built without NaN
+ * semantics, and the result for an inf or NaN input is not defined.
  *
  * `workspace` (device memory, caller-owned, no initial contents needed) of
  * unum_infllmv2_attn_stage1_workspace_size(...) bytes lets rows over 512 keys
@@ -79,8 +90,8 @@ int unum_abi_version(void);
  * log-sum-exps, then the scores); NULL or a smaller workspace runs the
  * whole-row kernel, with the same results to within fp32 rounding.  Batches
  * of at most two new tokens per sequence over rows of at most 4096 keys run
- * one workgroup per row and need no workspace.  Calls that share one
- * workspace must not overlap.
+ * one workgroup per row and leave the workspace unused.  Calls that share
+ * one workspace must not overlap.
  */
 int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                               const void* k, int64_t k_stride_t, int64_t k_stride_h,
@@ -91,8 +102,9 @@ int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int64_t q_strid
                               int32_t causal, void* workspace, int64_t workspace_bytes,
                               void* stream);
 
-/* Workspace bytes unum_infllmv2_attn_stage1 uses for this problem on the
- * current device (>= 0; 0: the problem is not split), with out_cols =
+/* Workspace bytes unum_infllmv2_attn_stage1 and
+ * unum_infllmv2_attn_stage1_maxpool use for this problem on the current
+ * device (>= 0; 0: rows of at most 512 keys, never split), with out_cols =
  * round_up(max_seqlen_k, 128).  B is the number of sequences. */
 int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t Hq,
                                                  int64_t Hkv, int64_t D,
@@ -112,8 +124,10 @@ int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t 
  *          keys run the key-split kernels, pooling in their second pass;
  *          NULL runs whole rows.
  * Other arguments as unum_infllmv2_attn_stage1 and unum_max_pooling_1d_varlen.
- * Only the MFMA paths (G = 16, D = 128, 16-byte aligned q/k, scale > 0) are
- * fused; other shapes return UNUM_ERR_UNSUPPORTED.
+ * Fused only on the key-streaming MFMA path: G = 16, D = 128, 16-byte
+ * aligned q/k, scale > 0 and out_cols > 512.  Every other problem --
+ * including rows of at most 512 keys -- returns UNUM_ERR_UNSUPPORTED; run
+ * unum_infllmv2_attn_stage1 and unum_max_pooling_1d_varlen there.
  */
 int unum_infllmv2_attn_stage1_maxpool(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                                       const void* k, int64_t k_stride_t, int64_t k_stride_h,

@@ -60,8 +60,17 @@ def infllmv2_attn_stage1(q, k, v, cu_seqlens_q, cu_seqlens_k, cu_seqlens_v=None,
                          max_seqlen_q=None, max_seqlen_k=None, dropout_p=0.0,
                          softmax_scale=None, causal=False, window_size=(-1, -1),
                          softcap=0.0, alibi_slopes=None, deterministic=False,
-                         return_attn_probs=True, block_table=None):
-    """fp32 scores ``[Hkv, Tq, round_up(max_seqlen_k, 128)]`` (CPU tensor)."""
+                         return_attn_probs=True, block_table=None, drop_past_cols=False):
+    """fp32 scores ``[Hkv, Tq, round_up(max_seqlen_k, 128)]`` (CPU tensor).
+
+    A sequence with more keys than the output has columns (a ``max_seqlen_k``
+    below a real length) makes the reference store past the row
+    (``_triton_v2.py:146-150``): undefined there, so this oracle raises --
+    unless ``drop_past_cols``, the build's documented contract for that input:
+    the visible count is computed from the real key count and then capped at
+    the column count, so each row is the softmax over its first
+    ``min(vis, Kp)`` keys (the dropped keys are in no denominator).
+    """
     q = q.detach().cpu()
     k = k.detach().cpu()
     Tq, Hq, D = q.shape
@@ -86,17 +95,19 @@ def infllmv2_attn_stage1(q, k, v, cu_seqlens_q, cu_seqlens_k, cu_seqlens_v=None,
         Lq, Lk = qe - qs, ke - ks
         if Lq <= 0 or Lk <= 0:
             continue
-        if Lk > Kp:
+        if Lk > Kp and not drop_past_cols:
             raise ValueError("sequence key length exceeds round_up(max_seqlen_k, 128)")
         vis = visible_counts(np.arange(Lq), Lq, Lk, causal)            # [Lq]
-        cols = np.arange(Lk)
-        masked = torch.from_numpy(cols[None, :] >= vis[:, None])       # [Lq, Lk]
+        vis = np.minimum(vis, Kp)
+        nk = min(Lk, Kp)                                                # keys scored
+        cols = np.arange(nk)
+        masked = torch.from_numpy(cols[None, :] >= vis[:, None])       # [Lq, nk]
         for g in range(Hkv):
             qg = qf[qs:qe, g * G:(g + 1) * G, :]                          # [Lq, G, D]
-            kg = kf[ks:ke, g, :]                                          # [Lk, D]
-            s = torch.matmul(qg, kg.t()) * scale                          # [Lq, G, Lk]
+            kg = kf[ks:ks + nk, g, :]                                     # [nk, D]
+            s = torch.matmul(qg, kg.t()) * scale                          # [Lq, G, nk]
             s = s.masked_fill(masked[:, None, :], -math.inf)
             p = torch.softmax(s, dim=-1)
             p = torch.nan_to_num(p, nan=0.0)
-            out[g, qs:qe, :Lk] = p.sum(dim=1)
+            out[g, qs:qe, :nk] = p.sum(dim=1)
     return out

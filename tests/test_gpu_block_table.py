@@ -5,7 +5,8 @@ import pytest
 import torch
 
 from oracle.block_table import get_block_table as oracle_bt
-from unum_ops_amd import workloads
+import workloads
+from unum_ops_amd import sparse_kernel_extension as ske
 from unum_ops_amd.sparse_kernel_extension import (get_block_table, get_block_table_v1,
                                                   get_block_table_v2, get_block_table_v3)
 
@@ -95,3 +96,59 @@ def test_pipeline_scale_properties(dev):
              token_pos_in_bs=pos, seqlen_q=torch.tensor([ctx], dtype=torch.int32))
     out = _run(d, dev)
     np.testing.assert_array_equal(out, _oracle(d))
+
+
+# Head multiplier of each exported name, as its reference function uses it:
+# the torch reference's constant kHeadGroup = 2 (get_table_torch.py:12), the
+# Triton functions' H (get_table_triton.py:259, :315, :364; the package
+# exports the first as get_block_table_v2/_v3, sparse_kernel_extension/
+# __init__.py:7-12).  get_block_table_v1 (compiled-only CUDA extension,
+# pinned by the reference tests at H = 2 only) takes 2 here.
+_MULTIPLIER = {
+    "get_block_table": "H",
+    "get_block_table_ref_torch": 2,
+    "get_block_table_ref_triton": "H",
+    "get_block_table_ref_triton_v2": "H",
+    "get_block_table_ref_triton_v3": "H",
+    "get_block_table_v1": 2,
+    "get_block_table_v2": "H",
+    "get_block_table_v3": "H",
+}
+
+
+def test_every_exported_name_has_a_multiplier():
+    assert sorted(_MULTIPLIER) == sorted(ske.__all__)
+
+
+@pytest.mark.parametrize("H", [1, 2, 3])
+@pytest.mark.parametrize("name", sorted(_MULTIPLIER))
+def test_alias_head_multiplier(name, H, dev):
+    g = torch.Generator().manual_seed(40 + H)
+    T, K, B, L = 29, 7, 4, 640
+    d = dict(topk_idx=torch.randint(-1, 10, (H, T, K), generator=g, dtype=torch.int32),
+             block_table=torch.randint(0, 1 << 20, (B, L), generator=g, dtype=torch.int32),
+             token_to_bs=torch.randint(0, B, (T,), generator=g, dtype=torch.int32),
+             token_pos_in_bs=torch.randint(1, L + 1, (T,), generator=g, dtype=torch.int32),
+             seqlen_q=torch.randint(1, L + 1, (B,), generator=g, dtype=torch.int32))
+    mult = H if _MULTIPLIER[name] == "H" else _MULTIPLIER[name]
+    got = _run(d, dev, getattr(ske, name))
+    np.testing.assert_array_equal(got, _oracle(d, head_group=mult))
+    if H != 2:  # the multiplier matters: the other one gives a different table
+        other = 2 if mult == H else H
+        assert not np.array_equal(got, _oracle(d, head_group=other))
+
+
+def test_cfg5_variant_16_1_slots(dev):
+    # The block-table stage of the Hq16/Hkv1 variant: H = 1, so the Triton
+    # names give slot + 0 (multiplier 1) and the torch name 2 * slot.
+    g = torch.Generator().manual_seed(11)
+    T, K = 512, 64
+    page = torch.randperm(2112, generator=g).to(torch.int32).view(1, 2112)
+    bt = workloads.expand_pages(page)
+    ids = torch.rand(1, T, 2112, generator=g).topk(K, dim=-1).indices.sort(-1).values.int()
+    pos = torch.arange(131072 + 1, 131072 + T + 1, dtype=torch.int32)
+    d = dict(topk_idx=ids, block_table=bt, token_to_bs=torch.zeros(T, dtype=torch.int32),
+             token_pos_in_bs=pos, seqlen_q=torch.tensor([135168], dtype=torch.int32))
+    np.testing.assert_array_equal(_run(d, dev, get_block_table_v2), _oracle(d, head_group=1))
+    np.testing.assert_array_equal(_run(d, dev, ske.get_block_table_ref_torch),
+                                  _oracle(d, head_group=2))

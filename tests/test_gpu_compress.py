@@ -8,7 +8,7 @@ import torch
 
 from oracle.compress import compress_keys as oracle_compress
 from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
-from unum_ops_amd import workloads
+import workloads
 from unum_ops_amd.compression import compress_keys
 from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1
 

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle.maxpool import max_pooling_1d_varlen as oracle_pool
-from unum_ops_amd import workloads
+import workloads
 from unum_ops_amd.infllm_v2 import max_pooling_1d_varlen, max_pooling_1d_varlen_ref_triton
 
 pytestmark = pytest.mark.gpu

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import oracle
-from unum_ops_amd import workloads
+import workloads
 from unum_ops_amd.pipeline import select_blocks, topk_blocks
 
 pytestmark = pytest.mark.gpu
@@ -51,8 +51,11 @@ def _check_pipeline(p, dev, min_recall):
 
     np.testing.assert_array_equal(idx_c.numpy(), topk_blocks(pooled_c, TOPK).numpy())
 
+    # select_blocks multiplies by H, as the reference's exported Triton
+    # functions do (get_table_triton.py:259).
     exp_t = oracle.get_block_table(idx_c, p["block_table"], p["token_to_bs"],
-                                   p["token_pos_in_bs"], p["seqlen_q"])
+                                   p["token_pos_in_bs"], p["seqlen_q"],
+                                   head_group=idx_c.shape[0])
     np.testing.assert_array_equal(table.cpu().numpy(), exp_t)
 
     # Selection agreement with the all-oracle pipeline.

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1, visible_counts
-from unum_ops_amd import workloads
+import workloads
 from unum_ops_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_triton,
                                     infllmv2_attn_stage1_triton_v2)
 

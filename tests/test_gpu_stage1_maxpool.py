@@ -13,7 +13,8 @@ import torch
 
 from oracle.maxpool import max_pooling_1d_varlen as oracle_pool
 from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
-from unum_ops_amd import _lib, workloads
+import workloads
+from unum_ops_amd import _lib
 from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1_maxpool
 
 pytestmark = pytest.mark.gpu

@@ -13,7 +13,7 @@ import torch
 
 from oracle.maxpool import max_pooling_1d_varlen as oracle_pool
 from oracle.topk import topk_blocks as oracle_topk
-from unum_ops_amd import workloads
+import workloads
 from unum_ops_amd.pipeline import maxpool_topk
 
 pytestmark = pytest.mark.gpu

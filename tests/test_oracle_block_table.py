@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 from oracle.block_table import get_block_table, get_block_table_bruteforce
-from unum_ops_amd import workloads
+import workloads
 
 
 def _rand_case(seed, H=2, T=5, K=3, B=3, L=200, scalar_pos=False, scalar_len=False):

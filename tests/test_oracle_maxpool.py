@@ -8,7 +8,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.maxpool import max_pooling_1d_varlen, max_pooling_1d_varlen_bruteforce
-from unum_ops_amd import workloads
+import workloads
 
 
 def _library_pool(x, cu_q, cu_k, cache, max_seqlen_q, max_context_len, local, init,

@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.stage1 import infllmv2_attn_stage1, tdiv, visible_counts
-from unum_ops_amd import workloads
+import workloads
 
 
 def _sdpa_reference(q, k, cu_q, cu_k, Hkv, causal, scale=None):
@@ -141,3 +141,32 @@ def test_output_columns_round_to_128():
                                 max_seqlen_k=lk + 200)
     assert out2.shape[-1] == 128 * math.ceil((lk + 200) / 128)
     torch.testing.assert_close(out2[..., :out.shape[-1]], out)
+
+
+def test_drop_past_cols_closed_form_and_sums():
+    # A max_seqlen_k below the real key count: the oracle raises by default;
+    # with drop_past_cols each row is the softmax over its first
+    # min(vis, Kp) keys.  q = 0 makes every kept score equal: G / min(vis, Kp)
+    # (a denominator that counted the dropped keys would give less), and a
+    # random q still gives rows summing to G.
+    Lq, Lk, max_k = 40, 700, 300
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(Lk, 2, 128, generator=g).to(torch.bfloat16)
+    cu_q = torch.tensor([0, Lq], dtype=torch.int32)
+    cu_k = torch.tensor([0, Lk], dtype=torch.int32)
+    q0 = torch.zeros(Lq, 32, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        infllmv2_attn_stage1(q0, k, None, cu_q, cu_k, max_seqlen_k=max_k, causal=True)
+    out = infllmv2_attn_stage1(q0, k, None, cu_q, cu_k, max_seqlen_k=max_k, causal=True,
+                               drop_past_cols=True)
+    kp = out.shape[-1]
+    assert kp == 384
+    vis = np.minimum(visible_counts(np.arange(Lq), Lq, Lk), kp)
+    assert vis.max() == kp and vis.min() > 0
+    j = np.arange(kp)[None, :]
+    exp = np.where(j < vis[:, None], 16.0 / vis[:, None], 0.0)
+    np.testing.assert_allclose(out[0].numpy(), exp, rtol=1e-6, atol=1e-7)
+    q = torch.randn(Lq, 32, 128, generator=g).to(torch.bfloat16)
+    out = infllmv2_attn_stage1(q, k, None, cu_q, cu_k, max_seqlen_k=max_k, causal=True,
+                               drop_past_cols=True)
+    np.testing.assert_allclose(out.sum(-1).numpy(), 16.0, rtol=1e-5)

@@ -1,4 +1,6 @@
-"""Seeded synthetic inputs for the benchmark configurations of the selection path.
+"""Seeded synthetic inputs for the benchmark configurations of the selection path
+(test and benchmark infrastructure: the GPU tests, `bench.py` and `smoke()` use it;
+the product package does not).
 
 All inputs come from ``torch.Generator('cpu').manual_seed(seed)`` and are CPU
 tensors; callers move them to the GPU.  The five configurations:

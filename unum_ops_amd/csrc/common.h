@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
@@ -46,18 +47,20 @@ __device__ __forceinline__ float wave_shr1(float v, float fill) {
                                                     0xF, 0xF, false));
 }
 
-// Compute units of the current device (cached per device; 256 if the query fails).
+// Compute units of the current device (cached per device; 256 if the query
+// fails).  The cache is read and written by any host thread that launches:
+// relaxed atomics make that race-free (every writer stores the same value).
 inline int num_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

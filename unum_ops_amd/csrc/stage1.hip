@@ -95,6 +95,19 @@ __device__ __forceinline__ RowInfo row_info(const Stage1Args& a, int64_t t) {
   return r;
 }
 
+// Keys of a sequence (first key ks, lk keys) that a buffer descriptor may
+// cover: none when ks is negative, never past the end of k, and at most
+// out_cols -- the columns past it are not computed, and the cap keeps the
+// descriptor's byte range ((keys-1)*k_st + D)*2 inside 32 bits on every path
+// that checks (out_cols + chunk)*k_st*2 < 2^31.  Whatever cu_seqlens_k holds,
+// no load reads outside k.
+__device__ __forceinline__ int64_t readable_keys(const Stage1Args& a, int64_t ks, int64_t lk) {
+  if (ks < 0 || ks >= a.Tk) return 0;
+  int64_t n = lk < a.Tk - ks ? lk : a.Tk - ks;
+  n = n < a.out_cols ? n : a.out_cols;
+  return n > 0 ? n : 0;
+}
+
 // Score stores are non-temporal: nothing re-reads the rows, and keeping them
 // out of the caches measured about 6% faster on the prefill shape.
 template <typename OutT>
@@ -940,8 +953,9 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     for (int k = 0; k < TW; ++k) qf[k] = load_q_frag(a, sg.qs + lq[k], sg.g);
 
     // K block of (sequence, group): keys [0, keys_ok) are readable.
-    const int64_t keys_ok = sg.lk < a.Tk - sg.ks ? sg.lk : a.Tk - sg.ks;
-    const __bf16* kbase = a.k + static_cast<int64_t>(sg.ks) * a.k_st + static_cast<int64_t>(sg.g) * a.k_sh;
+    const int64_t keys_ok = readable_keys(a, sg.ks, sg.lk);
+    const __bf16* kbase = a.k + (keys_ok > 0 ? static_cast<int64_t>(sg.ks) * a.k_st : 0) +
+                          static_cast<int64_t>(sg.g) * a.k_sh;
     const uint32_t k_bytes = keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u;
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(kbase, k_bytes);
 
@@ -1265,9 +1279,8 @@ template <int kWaves>
 __device__ __forceinline__ void row_k_issue(const Stage1Args& a, bf16x8* kt, const Segment& sg,
                                             int ntl, int wave) {
   const int lane = threadIdx.x & (kWave - 1);
-  int64_t keys_ok = sg.lk < a.Tk - sg.ks ? sg.lk : a.Tk - sg.ks;
+  int64_t keys_ok = readable_keys(a, sg.ks, sg.lk);
   keys_ok = keys_ok < 16 * ntl ? keys_ok : 16 * ntl;
-  if (sg.ks < 0) keys_ok = 0;
   const __bf16* kb = a.k + (keys_ok > 0 ? static_cast<int64_t>(sg.ks) * a.k_st : 0) +
                      static_cast<int64_t>(sg.g) * a.k_sh;
   const uint32_t bytes = keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u;
@@ -1796,8 +1809,9 @@ __global__ __launch_bounds__(kDecWaves* kWave) void stage1_decode_kernel(Stage1A
   const int64_t row = static_cast<int64_t>(pc.g) * a.Tq + pc.qs + pc.t0;
   OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
   // K block of (sequence, group): keys [0, keys_ok) are readable.
-  const int64_t keys_ok = pc.lk < a.Tk - pc.ks ? pc.lk : a.Tk - pc.ks;
-  const __bf16* kbase = a.k + static_cast<int64_t>(pc.ks) * a.k_st + static_cast<int64_t>(pc.g) * a.k_sh;
+  const int64_t keys_ok = readable_keys(a, pc.ks, pc.lk);
+  const __bf16* kbase = a.k + (keys_ok > 0 ? static_cast<int64_t>(pc.ks) * a.k_st : 0) +
+                        static_cast<int64_t>(pc.g) * a.k_sh;
   const __amdgpu_buffer_rsrc_t kr =
       make_rsrc(kbase, keys_ok > 0 ? static_cast<uint32_t>(((keys_ok - 1) * a.k_st + kD) * 2) : 0u);
   const Frag qf = load_q_frag(a, pc.qs + pc.t0, pc.g);
@@ -2033,7 +2047,9 @@ extern "C" int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t T
   if (Tq <= 0 || Hkv <= 0 || Hq != kG * Hkv || D != kD || max_seqlen_k <= 0) return 0;
   const int64_t out_cols = (max_seqlen_k + 127) / 128 * 128;
   if (out_cols <= kLdsTiles * 16) return 0;
-  if (Tq <= 2 * B && out_cols <= kDecMaxKeys) return 0;  // decode batches: one workgroup per row
+  // Decode batches (Tq <= 2B, at most 4096 columns) run the one-workgroup-a-row
+  // kernel in plain stage 1 and leave the workspace unused; the fused
+  // stage-1 + max-pool entry splits their keys with it.
   return split_plan(Hkv, Tq, B, out_cols).bytes;
 }
 

@@ -113,7 +113,7 @@ def maxpool_topk(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seqlen_q, ma
 def select_blocks(q, k, cu_seqlens_q, cu_seqlens_k, block_table, token_to_bs, token_pos_in_bs,
                   seqlen_q, max_context_len, *, max_seqlen_k=None, softmax_scale=None,
                   causal=True, topk=64, local_blocks=1, init_blocks=1, block_size=64,
-                  stride=16, head_group=2, return_intermediates=False):
+                  stride=16, head_group=None, return_intermediates=False):
     """Physical KV slots ``int32 [Tq, Hkv, topk * 64]`` of the blocks each query
     token attends to.
 
@@ -121,7 +121,9 @@ def select_blocks(q, k, cu_seqlens_q, cu_seqlens_k, block_table, token_to_bs, to
     ``cu_seqlens_q`` / ``cu_seqlens_k``; ``block_table [B, L]`` maps token
     positions of sequence b to slots; ``token_to_bs`` / ``token_pos_in_bs`` /
     ``seqlen_q`` are the block-table op's per-token and per-sequence inputs;
-    ``max_context_len`` sets the number of 64-token blocks.  With
+    ``max_context_len`` sets the number of 64-token blocks; ``head_group``
+    is the slot multiplier of ``get_block_table`` (default ``Hkv``, as the
+    reference's exported Triton functions use).  With
     ``return_intermediates`` the scores, pooled scores and block ids are
     returned too, as ``(table, scores, pooled, topk_idx)``.
     """
