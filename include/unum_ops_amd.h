@@ -111,6 +111,34 @@ int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t 
                                                  int64_t max_seqlen_k);
 
 /*
+ * unum_infllmv2_attn_stage1 without a caller workspace and without any
+ * allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Arguments and results are those
+ * of unum_infllmv2_attn_stage1 minus the workspace.
+ *
+ * The key-split workspace lives in a 4 MiB device array inside the library
+ * (one per device, held until the process ends).  Its address on a device is
+ * resolved on the first call there (with that device current); make that
+ * first call outside graph capture.  A problem whose key split needs more
+ * than 4 MiB returns UNUM_ERR_WORKSPACE without launching; the split plan
+ * keeps about six workgroups per CU, which bounds its workspace near
+ * 8 KiB per CU (about 2 MiB on a 256-CU MI355X), so on that GPU every
+ * problem fits.  Every
+ * call on one device shares that device's array: calls that overlap on one
+ * device (other streams, other threads) race and must be serialised by the
+ * caller.  Nothing in the array needs clearing: each call writes every
+ * element it reads before reading it.
+ */
+int unum_infllmv2_attn_stage1_noalloc(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                      const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                      void* out, int32_t out_dtype, int64_t B, int64_t Tq,
+                                      int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t max_seqlen_k, int64_t out_cols, float scale,
+                                      int32_t causal, void* stream);
+
+/*
  * Stage 1 with the max-pool fused into it.  No single reference function: it
  * equals max_pooling_1d_varlen (max_pooling_1d_varlen.py:127-183; block 64,
  * stride 16, cache_lens 0) applied to infllmv2_attn_stage1's fp32 scores with

@@ -45,6 +45,17 @@ SIGNATURES = {
         _p,                        # stream
     ]),
     "unum_infllmv2_attn_stage1_workspace_size": (_i64, [_i64] * 6),
+    "unum_infllmv2_attn_stage1_noalloc": (ctypes.c_int, [
+        _p, _i64, _i64,            # q, q_stride_t, q_stride_h
+        _p, _i64, _i64,            # k, k_stride_t, k_stride_h
+        _p, _p,                    # cu_seqlens_q, cu_seqlens_k
+        _p, _i32,                  # out, out_dtype
+        _i64, _i64, _i64,          # B, Tq, Tk
+        _i64, _i64, _i64,          # Hq, Hkv, D
+        _i64, _i64,                # max_seqlen_k, out_cols
+        ctypes.c_float, _i32,      # scale, causal
+        _p,                        # stream
+    ]),
     "unum_infllmv2_attn_stage1_maxpool": (ctypes.c_int, [
         _p, _i64, _i64,            # q, q_stride_t, q_stride_h
         _p, _i64, _i64,            # k, k_stride_t, k_stride_h

@@ -1908,6 +1908,14 @@ Stage1Path stage1_path(const Stage1Args& a) {
   return mfma ? kPathRowMfma : kPathGeneric;
 }
 
+// Decode batches (at most two new tokens per sequence on average, rows of at
+// most kDecMaxKeys keys) run stage1_decode_kernel on the streaming path.
+inline bool decode_batch(const Stage1Args& a) {
+  return a.Tq <= 2 * a.B && a.out_cols <= kDecMaxKeys &&
+         (a.out_cols + 64) * a.k_st * 2 < (int64_t{1} << 31) &&
+         piece_grid(a.Hkv, a.Tq, a.B, 1) <= INT32_MAX;
+}
+
 // Key-split plan of the streaming path: pieces of 2W tokens (W waves of two,
 // W from split_waves) times splits of `chunks` 64-key chunks, about six workgroups per CU in
 // all against the piece bound (measured on decode batches: four left CUs
@@ -2005,9 +2013,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
 #undef UNUM_LDS_CASE
       default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
     }
-  } else if (path == kPathStream && a.Tq <= 2 * a.B && a.out_cols <= kDecMaxKeys &&
-             (a.out_cols + 64) * a.k_st * 2 < (int64_t{1} << 31) &&
-             piece_grid(a.Hkv, a.Tq, a.B, 1) <= INT32_MAX) {
+  } else if (path == kPathStream && decode_batch(a)) {
     // Decode batches (at most two new tokens per sequence on average): one
     // workgroup per row, the waves splitting its keys.
     hipLaunchKernelGGL(stage1_decode_kernel<OutT>,
@@ -2157,4 +2163,80 @@ extern "C" int unum_infllmv2_attn_stage1_maxpool(
   pp.write_scores = scores != nullptr;
   return launch_stage1<float, true>(a, pp, workspace, workspace_bytes,
                                     static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------ stage 1 without allocation
+// The key-split workspace of unum_infllmv2_attn_stage1 held in a file-scope
+// device array, for callers that cannot allocate.  Each device that loads the
+// library holds its own copy of the array until the process ends.  In host
+// code `scratch` names a host-side stand-in: the kernels take the device
+// address that hipGetSymbolAddress returns for the current device, resolved
+// once per device on the first call there.
+namespace unum {
+namespace {
+constexpr int64_t kScratchBytes = int64_t{4} << 20;  // 4 MiB per device
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// This device's address of `scratch`, or nullptr (with the error set).
+void* scratch_ptr(const char* op) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no usable current device (%s)", op,
+              e != hipSuccess ? hipGetErrorString(e) : "device index out of range");
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr) {
+    set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", op, dev,
+              hipGetErrorString(e));
+    return nullptr;
+  }
+  // Racing first calls on one device store the same address.
+  g_scratch_ptr[dev].store(p, std::memory_order_release);
+  return p;
+}
+}  // namespace
+}  // namespace unum
+
+extern "C" int unum_infllmv2_attn_stage1_noalloc(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t,
+    int64_t k_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, void* out,
+    int32_t out_dtype, int64_t B, int64_t Tq, int64_t Tk, int64_t Hq, int64_t Hkv, int64_t D,
+    int64_t max_seqlen_k, int64_t out_cols, float scale, int32_t causal, void* stream) {
+  using namespace unum;
+  clear_error();
+  const char* op = "infllmv2_attn_stage1_noalloc";
+  Stage1Args a;
+  const int st = stage1_args(a, q, q_stride_t, q_stride_h, k, k_stride_t, k_stride_h,
+                             cu_seqlens_q, cu_seqlens_k, out, B, Tq, Tk, Hq, Hkv, D,
+                             max_seqlen_k, out_cols, scale, causal, op);
+  if (st != 0) return st < 0 ? st : UNUM_OK;
+  UNUM_REQUIRE(out, "%s: null output", op);
+  UNUM_REQUIRE(out_dtype == UNUM_DTYPE_F32 || out_dtype == UNUM_DTYPE_BF16,
+               "%s: unsupported out dtype %d", op, out_dtype);
+  // The workspace the plain entry point would split keys with; none for the
+  // paths that do not split (rows of at most 512 keys, decode batches).
+  const bool splits = out_dtype == UNUM_DTYPE_F32 ? stage1_path<float>(a) == kPathStream
+                                                  : stage1_path<uint16_t>(a) == kPathStream;
+  const int64_t need = splits && !decode_batch(a) ? split_plan(a.Hkv, a.Tq, a.B, a.out_cols).bytes : 0;
+  if (need > kScratchBytes)
+    UNUM_FAIL(UNUM_ERR_WORKSPACE,
+              "%s: this problem splits its keys over %lld bytes of workspace, more than the "
+              "%lld-byte device scratch array; call unum_infllmv2_attn_stage1 with a workspace",
+              op, (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_ptr(op);
+    if (ws == nullptr) return UNUM_ERR_LAUNCH;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (out_dtype == UNUM_DTYPE_F32)
+    return launch_stage1<float, false>(a, Stage1Pool{}, ws, need > 0 ? kScratchBytes : 0, s);
+  return launch_stage1<uint16_t, false>(a, Stage1Pool{}, ws, need > 0 ? kScratchBytes : 0, s);
 }
