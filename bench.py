@@ -43,7 +43,9 @@ def parse():
                                        "maxpool_cfg5", "maxpool_topk", "maxpool_topk_cfg5",
                                        "compress_keys_cfg5", "stage1_maxpool",
                                        "stage1_maxpool_cfg5", "stage1_cfg4", "stage1_decode",
-                                       "stage1_peaky", "copy"],
+                                       "stage1_peaky", "stage1_cfg5_h16", "maxpool_cfg5_h16",
+                                       "block_table_cfg5_h16", "block_table_cfg4",
+                                       "stage1_maxpool_cfg4", "copy"],
                     default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
@@ -103,6 +105,33 @@ def build_inputs(dev):
     c5["decode"] = dict(q=pd["q"].to(dev), k=pd["k"].to(dev), cu_q=pd["cu_seqlens_q"].to(dev),
                         cu_k=pd["cu_seqlens_k"].to(dev), max_seqlen_k=pd["max_seqlen_k"],
                         cu_q_cpu=pd["cu_seqlens_q"], cu_k_cpu=pd["cu_seqlens_k"])
+    # cfg5's Hq16/Hkv1 variant through the same stages (H = 1 everywhere).
+    p6 = workloads.cfg5_pipeline(Hq=16, Hkv=1)
+    q6, k6 = p6["q"].to(dev), p6["k"].to(dev)
+    sc6 = infllmv2_attn_stage1(q6, k6, None, cu_q5, cu_k5, max_seqlen_k=p6["max_seqlen_k"],
+                               causal=True)
+    pooled6 = max_pooling_1d_varlen(sc6, cu_q5, cu_k5, torch.zeros(1, dtype=torch.int32, device=dev),
+                                    max_seqlen_q=16 * sc6.shape[-1],
+                                    max_context_len=p6["max_context_len"], local_blocks=1,
+                                    init_blocks=1)
+    c5["h16"] = dict(q=q6, k=k6, scores=sc6, max_seqlen_k=p6["max_seqlen_k"],
+                     bt=dict(topk_idx=topk_blocks(pooled6, 64), block_table=bt["block_table"],
+                             token_to_bs=bt["token_to_bs"], token_pos_in_bs=bt["token_pos_in_bs"],
+                             seqlen_q=bt["seqlen_q"]))
+    del pooled6
+    # cfg4's block-table stage: its stage 1, max-pool and top-64 run once here.
+    sc4 = infllmv2_attn_stage1(c4["q"], c4["k"], None, c4["cu_q"], c4["cu_k"],
+                               max_seqlen_k=c4["max_seqlen_k"], causal=True)
+    pooled4 = max_pooling_1d_varlen(sc4, c4["cu_q"], c4["cu_k"],
+                                    torch.zeros(64, dtype=torch.int32, device=dev),
+                                    max_seqlen_q=16 * sc4.shape[-1],
+                                    max_context_len=p4["max_context_len"], local_blocks=1,
+                                    init_blocks=1)
+    c4["max_context_len"] = p4["max_context_len"]
+    c4["bt"] = dict(topk_idx=topk_blocks(pooled4, 64), block_table=p4["block_table"].to(dev),
+                    token_to_bs=p4["token_to_bs"].to(dev),
+                    token_pos_in_bs=p4["token_pos_in_bs"].to(dev), seqlen_q=p4["seqlen_q"].to(dev))
+    del sc4, pooled4
     torch.cuda.synchronize()
     log(f"cfg4/cfg5 inputs ready ({time.time() - t0:.1f}s)")
     return s1, s1g, mp, mpg, bt, c5
@@ -203,6 +232,33 @@ def main():
     def op_compress_cfg5():
         return compress_keys(c5["raw"], c5["cu_raw"], plan=plan5)
 
+    h16 = c5["h16"]
+
+    def op_stage1_cfg5_h16():
+        return infllmv2_attn_stage1(h16["q"], h16["k"], None, c5["cu_q"], c5["cu_k"],
+                                    max_seqlen_k=h16["max_seqlen_k"], causal=True)
+
+    def op_maxpool_cfg5_h16():
+        return max_pooling_1d_varlen(h16["scores"], c5["cu_q"], c5["cu_k"], c5["cache"],
+                                     max_seqlen_q=16 * h16["scores"].shape[-1],
+                                     max_context_len=c5["max_context_len"], local_blocks=1,
+                                     init_blocks=1)
+
+    def op_block_table_cfg5_h16():
+        b = h16["bt"]
+        return get_block_table(b["topk_idx"], b["block_table"], b["token_to_bs"],
+                               b["token_pos_in_bs"], b["seqlen_q"])
+
+    def op_block_table_cfg4():
+        b = c4["bt"]
+        return get_block_table(b["topk_idx"], b["block_table"], b["token_to_bs"],
+                               b["token_pos_in_bs"], b["seqlen_q"])
+
+    def op_stage1_maxpool_cfg4():
+        return infllmv2_attn_stage1_maxpool(c4["q"], c4["k"], c4["cu_q"], c4["cu_k"],
+                                            c4["max_context_len"],
+                                            max_seqlen_k=c4["max_seqlen_k"], causal=True)
+
     ops = [("stage1", op_stage1), ("maxpool", op_maxpool), ("block_table", op_block_table)]
     # Timed per kernel only: the long-context configuration's stage 1 and
     # max-pool, the fused pool + top-64 selection on both pool inputs, and key
@@ -211,7 +267,11 @@ def main():
              ("maxpool_topk", op_topk), ("maxpool_topk_cfg5", op_topk_cfg5),
              ("compress_keys_cfg5", op_compress_cfg5), ("stage1_maxpool", op_stage1_maxpool),
              ("stage1_maxpool_cfg5", op_stage1_maxpool_cfg5), ("stage1_cfg4", op_stage1_cfg4),
-             ("stage1_decode", op_stage1_decode), ("stage1_peaky", op_stage1_peaky)]
+             ("stage1_decode", op_stage1_decode), ("stage1_peaky", op_stage1_peaky),
+             ("stage1_cfg5_h16", op_stage1_cfg5_h16), ("maxpool_cfg5_h16", op_maxpool_cfg5_h16),
+             ("block_table_cfg5_h16", op_block_table_cfg5_h16),
+             ("block_table_cfg4", op_block_table_cfg4),
+             ("stage1_maxpool_cfg4", op_stage1_maxpool_cfg4)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -340,7 +400,41 @@ def main():
                                config=("cfg2 input" if name == "maxpool_topk" else "cfg5 scores")
                                + " -> top-64 block ids int32 [2, T, 64]")
 
-    for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5")):
+    if "stage1_cfg5_h16" in per_op:
+        flop, nbytes, _ = workloads.stage1_work(c5["cu_q_cpu"], c5["cu_k_cpu"], 16, 1, 128,
+                                                h16["scores"].shape[-1])
+        t = per_op["stage1_cfg5_h16"] * 1e-3
+        comps["stage1_cfg5_h16"] = dict(us=per_op["stage1_cfg5_h16"] * 1e3, tflops=flop / t / 1e12,
+                                        pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                                        gbs=nbytes / t / 1e9,
+                                        pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                        flop=flop, bytes=nbytes, bound="mfma",
+                                        config="cfg5 Hq16/Hkv1 variant, fp32 out [1,4096,8448]")
+    if "maxpool_cfg5_h16" in per_op:
+        nbytes = workloads.maxpool_bytes(c5["cu_q_cpu"], c5["cu_k_cpu"], [0], 1,
+                                         -(-c5["max_context_len"] // 64))
+        t = per_op["maxpool_cfg5_h16"] * 1e-3
+        comps["maxpool_cfg5_h16"] = dict(us=per_op["maxpool_cfg5_h16"] * 1e3, gbs=nbytes / t / 1e9,
+                                         pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                         bytes=nbytes,
+                                         config="cfg5 Hq16/Hkv1 scores fp32 [1,4096,8448] -> [1,4096,2112]")
+    for name, b, T, B, cfg in (
+            ("block_table_cfg5_h16", h16["bt"], 4096, 1,
+             "cfg5 Hq16/Hkv1 block-table stage: T=4096 H=1 K=64 -> int32 [4096,1,4096]"),
+            ("block_table_cfg4", c4["bt"], int(c4["cu_q_cpu"][-1]), 64,
+             f"cfg4 block-table stage: T={int(c4['cu_q_cpu'][-1])} H=2 K=64, 64 sequences "
+             f"-> int32 [{int(c4['cu_q_cpu'][-1])},2,4096] (latency-bound)")):
+        if name in per_op:
+            H = b["topk_idx"].shape[0]
+            nbytes = workloads.block_table_bytes(b["topk_idx"].cpu(), b["token_to_bs"].cpu(), H, T,
+                                                 64, B)
+            t = per_op[name] * 1e-3
+            comps[name] = dict(us=per_op[name] * 1e3, gbs=nbytes / t / 1e9,
+                               pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
+                               config=cfg)
+
+    for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5"),
+                      ("stage1_maxpool_cfg4", "stage1_cfg4")):
         if name in per_op and src in comps:
             flop = comps[src]["flop"]
             t = per_op[name] * 1e-3
@@ -362,7 +456,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline and "stage1" in comps:
-        cpu = cpu_baseline(s1)
+        cpu = cpu_baseline(s1, mp, bt)
 
     s1c = comps.get("stage1")
     line = {
@@ -389,7 +483,8 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(s1c["gbs"], 1),
                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": round(s1c["gbs"] / PEAK_HBM_GBS, 4),
-                            "traffic": profiled_traffic("stage1_cfg3.txt"),
+                            "traffic": profiled_traffic("stage1_cfg3.txt",
+                                                        "unum_ops_amd/csrc/stage1.hip"),
                             "kernel": "stage1 (cfg3)",
                             "mfma_frac": round(s1c["tflops"] / PEAK_BF16_TFLOPS, 4)}
     line["cpu_baseline"] = cpu
@@ -410,47 +505,129 @@ def calibration_copy(dev, args):
     print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n}), flush=True)
 
 
-def profiled_traffic(name):
+def source_digest(rel):
+    """sha256 (first 16 hex digits) of a repository file."""
+    import hashlib
+
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), rel), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def profiled_traffic(name, source):
     """HBM bytes per launch of a kernel, as measured with the FETCH_SIZE and
-    WRITE_SIZE counters (copy-calibrated) and recorded in profiles/<name>;
-    None when that summary is absent."""
+    WRITE_SIZE counters (copy-calibrated) and recorded in profiles/<name>.
+    The summary records the sha256 of the kernel's source it was measured
+    on; when that source has changed since, or the summary is absent, the
+    reading no longer describes this build and None is returned."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    traffic, digest = None, None
     try:
         with open(path) as f:
             for row in f:
                 if row.startswith("traffic_bytes_per_launch:"):
-                    return int(float(row.split(":", 1)[1].split()[0]))
+                    traffic = int(float(row.split(":", 1)[1].split()[0]))
+                elif row.startswith("source_sha256:"):
+                    digest = row.split(":", 1)[1].split()[0]
+    except OSError:
+        return None
+    if digest is None or digest != source_digest(source):
+        log(f"profiles/{name} was measured on another {source}: traffic not reported")
+        return None
+    return traffic
+
+
+def host_cpu():
+    """The host's CPU model, physical cores and the CPUs this process may use."""
+    model, cores = None, set()
+    phys = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for row in f:
+                key, _, val = row.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model is None:
+                    model = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    cores.add((phys, val))
     except OSError:
         pass
-    return None
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return {"cpu_model": model, "physical_cores": len(cores) or None, "cpus_available": avail}
 
 
-def cpu_baseline(s1):
-    """The CPU oracle (torch fp32, the reference algorithm restated) on the
-    whole cfg3 workload, repeated for about 10 s; the median run is reported."""
+def _median_time(fn, budget_s, min_runs=3):
+    times = []
+    t_end = time.time() + budget_s
+    while len(times) < min_runs or time.time() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def cpu_baseline(s1, mp, bt):
+    """The CPU oracle -- the reference algorithm of each op restated in torch /
+    numpy (oracle/) -- on this host, median of bounded repeated runs:
+
+    * stage 1 (the headline unit, TFLOP/s): torch fp32 on every thread the
+      process may use, the whole cfg3 workload, about 10 s;
+    * max-pool (GB/s): the numpy restatement of the reference's Triton kernel
+      (max_pooling_1d_varlen.py:33-183; the reference has no torch version)
+      on the whole cfg2 input, one thread, at least 3 runs;
+    * block table (GB/s): the numpy restatement of get_block_table_ref_torch
+      (get_table_torch.py:4-44, same gather-then-where steps) on the whole
+      cfg5 block-table stage, one thread, at least 3 runs.
+    """
     import torch
 
+    import oracle
     from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
     from tests import workloads
 
-    torch.set_num_threads(os.cpu_count() or 1)
+    host = host_cpu()
+    threads = host["cpus_available"] or os.cpu_count() or 1
+    torch.set_num_threads(threads)
     flop, _, _ = workloads.stage1_work(s1["cu_seqlens_q"], s1["cu_seqlens_k"], 32, 2, 128, 512)
     oracle_stage1(s1["q"][:512], s1["k"][:511], None, torch.tensor([0, 512], dtype=torch.int32),
                   torch.tensor([0, 511], dtype=torch.int32), max_seqlen_k=511,
                   causal=True)                                          # warm-up
-    times = []
-    t_end = time.time() + 10
-    while len(times) < 3 or time.time() < t_end:
-        t0 = time.perf_counter()
-        oracle_stage1(s1["q"], s1["k"], None, s1["cu_seqlens_q"], s1["cu_seqlens_k"],
-                      max_seqlen_k=s1["max_seqlen_k"], causal=True)
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    log(f"cpu baseline: {med:.2f} s per cfg3 pass ({len(times)} runs)")
-    return {"value": round(flop / med / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": "oracle stage 1 (torch fp32 CPU) on the whole cfg3 workload (4 x 8192 "
-                      f"tokens), median of {len(times)} runs"}
+    med, n = _median_time(lambda: oracle_stage1(
+        s1["q"], s1["k"], None, s1["cu_seqlens_q"], s1["cu_seqlens_k"],
+        max_seqlen_k=s1["max_seqlen_k"], causal=True), 10)
+    log(f"cpu baseline: stage 1 {med:.2f} s per cfg3 pass ({n} runs, {threads} threads)")
+    line = {"value": round(flop / med / 1e12, 5), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle stage 1 (torch fp32 CPU) on the whole cfg3 workload (4 x 8192 "
+                      f"tokens), median of {n} runs", **host}
+
+    mp_bytes = workloads.maxpool_bytes(mp["cu_seqlens_q"], mp["cu_seqlens_k"], mp["cache_lens"],
+                                       2, 256)
+    med, n = _median_time(lambda: oracle.max_pooling_1d_varlen(
+        mp["input"], mp["cu_seqlens_q"], mp["cu_seqlens_k"], mp["cache_lens"],
+        mp["max_seqlen_q"], mp["max_context_len"], mp["local_blocks"], mp["init_blocks"]), 5)
+    log(f"cpu baseline: max-pool {med:.2f} s per cfg2 pass ({n} runs)")
+    comps = {"maxpool": {"value": round(mp_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+                         "kind": "port",
+                         "sample": "numpy restatement of the reference's Triton max-pool "
+                                   "(the reference ships no torch version) on the whole cfg2 "
+                                   f"input, median of {n} runs"}}
+
+    ids, table = bt["topk_idx"].cpu(), bt["block_table"].cpu()
+    tok, pos, slen = bt["token_to_bs"].cpu(), bt["token_pos_in_bs"].cpu(), bt["seqlen_q"].cpu()
+    bt_bytes = workloads.block_table_bytes(ids, tok, 2, 4096, 64, 1)
+    med, n = _median_time(lambda: oracle.get_block_table(ids, table, tok, pos, slen), 5)
+    log(f"cpu baseline: block table {med:.2f} s per cfg5 stage ({n} runs)")
+    comps["block_table"] = {"value": round(bt_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
+                            "kind": "port",
+                            "sample": "numpy restatement of get_block_table_ref_torch on the "
+                                      f"whole cfg5 block-table stage, median of {n} runs"}
+    line["components"] = comps
+    return line
 
 
 if __name__ == "__main__":

@@ -1191,15 +1191,19 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             nb[k][rr] = L > 0.f ? -(M * c + __builtin_amdgcn_logf(L)) : -INFINITY;
           }
         if constexpr (kSplit == 1) {
-          // This split's log2-sum-exp per (row, head): lane 16g + j (j < 4)
-          // writes head 4g + j.
+          // This split's log2-sum-exp per (row, head): lane 16g + rr (rr < 4)
+          // writes head 4g + rr -- one store per head slot, so nb stays in
+          // registers (a lane-dependent pick among nb[k][0..3] would be
+          // lowered to a dynamically indexed stack array).
           const int j = lane & 15;
 #pragma unroll
           for (int k = 0; k < TW; ++k) {
-            const float v = j == 0 ? nb[k][0] : j == 1 ? nb[k][1] : j == 2 ? nb[k][2] : nb[k][3];
-            if (own[k] && j < 4)  // nb = -inf: no visible key, log2-sum-exp -inf
-              sp.ws[ws_row(k) + static_cast<int64_t>(split) * R * 16 + 4 * (lane >> 4) + j] =
-                  v == -INFINITY ? -INFINITY : -v;
+            float* dst = sp.ws + ws_row(k) + static_cast<int64_t>(split) * R * 16 + 4 * (lane >> 4);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const float v = nb[k][rr];  // -inf: no visible key, log2-sum-exp -inf
+              if (own[k] && j == rr) dst[rr] = v == -INFINITY ? -INFINITY : -v;
+            }
           }
         }
       }
