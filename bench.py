@@ -45,7 +45,8 @@ def parse():
                                        "stage1_maxpool_cfg5", "stage1_cfg4", "stage1_decode",
                                        "stage1_peaky", "stage1_cfg5_h16", "maxpool_cfg5_h16",
                                        "block_table_cfg5_h16", "block_table_cfg4",
-                                       "stage1_maxpool_cfg4", "copy"],
+                                       "stage1_maxpool_cfg4", "stage2_cfg5", "stage2_cfg4",
+                                       "copy"],
                     default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
@@ -132,6 +133,14 @@ def build_inputs(dev):
                     token_to_bs=p4["token_to_bs"].to(dev),
                     token_pos_in_bs=p4["token_pos_in_bs"].to(dev), seqlen_q=p4["seqlen_q"].to(dev))
     del sc4, pooled4
+    # Stage 2 over the selections above: random bf16 paged K/V caches of the
+    # configurations' page pools ([pages, 64, Hkv, 128]; cfg5 2112 pages,
+    # 138 MB per cache; cfg4 65536 pages, 2.1 GB per cache).
+    gen = torch.Generator(device=dev).manual_seed(2)
+    c5["kv"] = [torch.randn(2112, 64, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+                for _ in range(2)]
+    c4["kv"] = [torch.randn(65536, 64, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
+                for _ in range(2)]
     torch.cuda.synchronize()
     log(f"cfg4/cfg5 inputs ready ({time.time() - t0:.1f}s)")
     return s1, s1g, mp, mpg, bt, c5
@@ -152,6 +161,7 @@ def main():
     from unum_ops_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_maxpool,
                                         max_pooling_1d_varlen)
     from unum_ops_amd.pipeline import maxpool_topk
+    from unum_ops_amd.sparse_attention import sparse_paged_attention
     from unum_ops_amd.sparse_kernel_extension import get_block_table
 
     dev = torch.device("cuda:0")
@@ -254,6 +264,17 @@ def main():
         return get_block_table(b["topk_idx"], b["block_table"], b["token_to_bs"],
                                b["token_pos_in_bs"], b["seqlen_q"])
 
+    def op_stage2_cfg5():
+        return sparse_paged_attention(c5["q"], c5["kv"][0], c5["kv"][1], 32, 2, 128 ** -0.5,
+                                      bt["topk_idx"], bt["block_table"], bt["token_to_bs"],
+                                      bt["token_pos_in_bs"], bt["seqlen_q"])
+
+    def op_stage2_cfg4():
+        b = c4["bt"]
+        return sparse_paged_attention(c4["q"], c4["kv"][0], c4["kv"][1], 32, 2, 128 ** -0.5,
+                                      b["topk_idx"], b["block_table"], b["token_to_bs"],
+                                      b["token_pos_in_bs"], b["seqlen_q"])
+
     def op_stage1_maxpool_cfg4():
         return infllmv2_attn_stage1_maxpool(c4["q"], c4["k"], c4["cu_q"], c4["cu_k"],
                                             c4["max_context_len"],
@@ -271,7 +292,8 @@ def main():
              ("stage1_cfg5_h16", op_stage1_cfg5_h16), ("maxpool_cfg5_h16", op_maxpool_cfg5_h16),
              ("block_table_cfg5_h16", op_block_table_cfg5_h16),
              ("block_table_cfg4", op_block_table_cfg4),
-             ("stage1_maxpool_cfg4", op_stage1_maxpool_cfg4)]
+             ("stage1_maxpool_cfg4", op_stage1_maxpool_cfg4),
+             ("stage2_cfg5", op_stage2_cfg5), ("stage2_cfg4", op_stage2_cfg4)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -432,6 +454,24 @@ def main():
             comps[name] = dict(us=per_op[name] * 1e3, gbs=nbytes / t / 1e9,
                                pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
                                config=cfg)
+
+    for name, b, nseq, cfg in (
+            ("stage2_cfg5", bt, 1, "cfg5 selection: T=4096, Hq32/Hkv2, top-64 blocks of 64 tokens, "
+                                   "paged bf16 K/V [2112,64,2,128], bf16 out [4096,32,128]"),
+            ("stage2_cfg4", c4["bt"], 64, "cfg4 selection: 64 sequences, Hq32/Hkv2, top-64, paged "
+                                         "bf16 K/V [65536,64,2,128], bf16 out")):
+        if name in per_op:
+            nbytes, flop, n_ent = workloads.sparse_attn_work(b["topk_idx"], b["token_to_bs"],
+                                                             b["token_pos_in_bs"], b["seqlen_q"],
+                                                             nseq)
+            t = per_op[name] * 1e-3
+            comps[name] = dict(us=per_op[name] * 1e3, gbs=nbytes / t / 1e9,
+                               pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                               tflops=flop / t / 1e12,
+                               pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                               bytes=nbytes, flop=flop, entries=n_ent, bound="hbm",
+                               config=cfg + " (bytes: each attended K and V row gathered once "
+                                            "per token and kv head, q, out)")
 
     for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5"),
                       ("stage1_maxpool_cfg4", "stage1_cfg4")):

@@ -247,6 +247,51 @@ int unum_get_block_table(const int32_t* topk_idx, int64_t topk_stride_h,
                          int64_t L, int32_t head_group, void* stream);
 
 /*
+ * Stage-2 sparse attention over the KV slots of the block table.  No
+ * portable reference function: the reference's consumer of get_block_table's
+ * output is an NPU paged-attention operator (test/test_pa.py:48-71,
+ * torch_npu._npu_paged_attention(query, key_cache, value_cache, num_heads,
+ * num_kv_heads, scale_value, block_table, context_lens, out); shapes
+ * test/test_pa.py:75-80).  This is the attention those slots define.
+ *
+ *   q            bf16 [T, Hq, D], element strides (q_stride_t, q_stride_h, 1)
+ *   key_cache, value_cache  bf16, viewed as n_rows rows of D elements, row r at
+ *                element r * kv_row_stride -- a [num_blocks, block_size,
+ *                Hkv, D] cache has n_rows = num_blocks*block_size*Hkv, and row
+ *                s*Hkv + h holds token slot s, kv head h
+ *   topk_idx     int32 [Hkv, T, K] block ids, element strides (h, t, k)
+ *   block_table  int32 [B, L] token-granular table, row stride bt_stride_b
+ *                (unused when `slots` is given)
+ *   slots        optional int32 [T, Hkv, K*64] contiguous: get_block_table's
+ *                output for these inputs with head_group = Hkv (NULL: the
+ *                slots are computed from block_table)
+ *   token_to_bs, token_pos_in_bs (T or 1 entries), seqlen_q (>= B or 1)
+ *                as for unum_get_block_table
+ *   out          [T, Hq, D] contiguous, out_dtype BF16 or F32
+ *
+ * For token t and kv head h, entry (t, h, 64k + o) is attended when the block
+ * table marks it valid (p = topk_idx[h,t,k]*64 + o, wrapping int32; b =
+ * token_to_bs[t] in [0, B); 0 <= p < seqlen_q[b]; p < token_pos_in_bs[t])
+ * and its row -- slots[t,h,64k+o], or Hkv*block_table[b, min(p, L-1)] + h
+ * (wrapping int32) -- lies in [0, n_rows).  Then
+ *   out[t, h*G+i] = sum_j softmax_j(scale * q[t,h*G+i] . K[row_j]) V[row_j]
+ * over the attended entries (repeats counted), fp32 math, and 0 when (t, h)
+ * has none.  G = Hq / Hkv must be 16 and D 128; K <= 64; q, the caches and
+ * out 16-byte aligned.
+ */
+int unum_sparse_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                const void* key_cache, const void* value_cache,
+                                int64_t kv_row_stride, int64_t n_rows, const int32_t* topk_idx,
+                                int64_t topk_stride_h, int64_t topk_stride_t,
+                                int64_t topk_stride_k, const int32_t* block_table,
+                                int64_t bt_stride_b, const int32_t* slots,
+                                const int32_t* token_to_bs, const int32_t* token_pos_in_bs,
+                                int64_t pos_numel, const int32_t* seqlen_q, int64_t seqlen_numel,
+                                void* out, int32_t out_dtype, int64_t T, int64_t Hq, int64_t Hkv,
+                                int64_t D, int64_t K, int64_t B, int64_t L, float scale,
+                                void* stream);
+
+/*
  * Key compression: mean-pool raw keys into the compressed keys stage 1 takes.
  * No reference function: the reference's stage 1 receives compressed keys;
  * the pooling (kernel 32, stride 16) is the one its benchmark configurations

@@ -253,3 +253,30 @@ def block_table_bytes(topk_idx, token_to_bs, H, T, K, B):
     pairs = torch.unique(torch.stack([bs[valid].long(), idx[valid].long()], 0), dim=1)
     U = pairs.shape[1]
     return 4 * T * H * K * 64 + 4 * H * T * K + 256 * U + 4 * (2 * T + B)
+
+
+def sparse_attn_work(topk_idx, token_to_bs, token_pos_in_bs, seqlen_q, num_seqs, G=16, D=128,
+                     out_bytes=2):
+    """Stage-2 sparse attention: (algorithmic HBM bytes, useful FLOP, attended entries).
+
+    Bytes: every attended entry's K row and V row gathered once per (token, kv
+    head) (``2 * 2 * D`` bytes), the queries read once and the output written
+    once.  FLOP: ``2 * G * D`` for the scores plus ``2 * G * D`` for P.V per
+    attended entry.  An entry is attended as the block table marks it valid
+    (``get_table_torch.py:18-33``)."""
+    idx = topk_idx.detach().cpu().to(torch.int64)              # [H, T, K]
+    H, T, K = idx.shape
+    bs = token_to_bs.detach().cpu().to(torch.int64).reshape(-1)
+    pos = token_pos_in_bs.detach().cpu().to(torch.int64).reshape(-1)
+    sl = seqlen_q.detach().cpu().to(torch.int64).reshape(-1)
+    ok = (bs >= 0) & (bs < num_seqs)
+    lim_s = sl.expand(T) if sl.numel() == 1 else sl[bs.clamp(0, num_seqs - 1)]
+    lim_p = pos.expand(T) if pos.numel() == 1 else pos
+    lim = torch.where(ok, torch.minimum(lim_s, lim_p), torch.zeros_like(lim_s))   # [T]
+    p0 = idx * PAGE                                             # [H, T, K]
+    # entries p0 + o (o < 64) with 0 <= p < lim
+    lo = p0.clamp(min=0)
+    hi = torch.minimum(p0 + PAGE, lim[None, :, None])
+    n = (hi - lo).clamp(min=0).sum().item()
+    nbytes = n * 2 * 2 * D + T * H * G * D * 2 + T * H * G * D * out_bytes
+    return float(nbytes), float(n * 4 * G * D), int(n)

@@ -9,6 +9,7 @@ A from-scratch, MI355X-native replacement for the selection path of
 * ``unum_ops_amd.pipeline.select_blocks``               (stage1 -> pool -> top-k -> table)
 * ``unum_ops_amd.pipeline.maxpool_topk``                (fused pool + block top-k)
 * ``unum_ops_amd.compression.compress_keys``            (raw keys -> compressed keys)
+* ``unum_ops_amd.sparse_attention.sparse_paged_attention`` (stage 2 over the block table)
 
 Each op keeps the reference's names, argument lists and output layouts and
 runs hand-written HIP kernels through the C ABI in ``include/unum_ops_amd.h``.
@@ -16,8 +17,10 @@ runs hand-written HIP kernels through the C ABI in ``include/unum_ops_amd.h``.
 
 import torch  # noqa: F401  -- load torch's HIP runtime before the native library
 
-from . import compression, infllm_v2, pipeline, sparse_kernel_extension  # noqa: E402
+from . import (compression, infllm_v2, pipeline, sparse_attention,  # noqa: E402
+               sparse_kernel_extension)
 
 __version__ = "0.1.0"
 
-__all__ = ["compression", "infllm_v2", "pipeline", "sparse_kernel_extension", "__version__"]
+__all__ = ["compression", "infllm_v2", "pipeline", "sparse_attention", "sparse_kernel_extension",
+           "__version__"]

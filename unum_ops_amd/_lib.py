@@ -96,6 +96,19 @@ SIGNATURES = {
         _i32, _i32, _i32,          # kernel_size, stride, windows_per_unit
         _p,                        # stream
     ]),
+    "unum_sparse_paged_attention": (ctypes.c_int, [
+        _p, _i64, _i64,            # q, q_stride_t, q_stride_h
+        _p, _p, _i64, _i64,        # key_cache, value_cache, kv_row_stride, n_rows
+        _p, _i64, _i64, _i64,      # topk_idx + strides (h, t, k)
+        _p, _i64,                  # block_table, row stride
+        _p,                        # slots (may be NULL)
+        _p, _p, _i64,              # token_to_bs, token_pos_in_bs, numel
+        _p, _i64,                  # seqlen_q, numel
+        _p, _i32,                  # out, out_dtype
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # T, Hq, Hkv, D, K, B, L
+        ctypes.c_float,            # scale
+        _p,                        # stream
+    ]),
     "unum_get_block_table": (ctypes.c_int, [
         _p, _i64, _i64, _i64,      # topk_idx + strides (h, t, k)
         _p, _i64,                  # block_table, row stride

@@ -1,0 +1,433 @@
+// Stage-2 sparse attention over the block table's KV slots, on gfx950.
+//
+// For token t and kv head h (G = 16 query heads per kv head, D = 128), the
+// keys are the entries (t, h, 64k + o) of get_block_table's output
+// (src/unum_ops/sparse_kernel_extension/get_table_torch.py:4-44,
+// get_table_triton.py:6-67): entry p = topk_idx[h, t, k]*64 + o (wrapping
+// int32) is attended when 0 <= p < seqlen_q[b] and p < token_pos_in_bs[t]
+// (b = token_to_bs[t] in [0, B)), and its KV row is the slot
+// Hkv * block_table[b, min(p, L-1)] + h -- row `slot` of the cache viewed as
+// [-1, D], i.e. token slot block_table[b, p], head h of a [num_blocks,
+// block_size, Hkv, D] cache -- or, given a precomputed slot table, that
+// table's entry.  Rows outside the cache are not attended.  Then
+//   out[t, h*16 + i] = softmax_j(scale * q[t, h*16+i] . K[row_j]) @ V[rows]
+// (0 when no entry is attended).  The reference's consumer of the table is an
+// NPU paged-attention operator (test/test_pa.py:48-71); this is its
+// arithmetic on the slots the table lists.
+//
+// One wave per (t, h).  Phase 1 stages the row of each of the K*64 entries
+// (or -1) in LDS and marks which 16-key stages hold an attended entry.
+// Phase 2 streams those stages through a ring of LDS buffers: each stage's
+// 16 K rows and 16 V rows (8 KiB) are gathered by buffer-free global-to-LDS
+// loads, issued kRing-1 stages ahead of the one being computed.  Per stage:
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (keys as M, heads as N), so a
+//     lane holds four keys of one head: the online-softmax state (max, sum)
+//     is one head per lane and needs no transposes;
+//   * P^T (bf16) is, as it stands in the accumulator layout, the B operand of
+//     v_mfma_f32_16x16x16_bf16 for O^T += V^T P^T; V^T fragments come from the
+//     row-major V rows in LDS through ds_read_b64_tr_b16 (transposing reads);
+//   * the running max moves only when a stage's max exceeds it by more than
+//     8 (log2 units), so the O^T rescale is rare; exponentials stay <= 2^8.
+#include "common.h"
+
+namespace unum {
+namespace {
+
+constexpr float kSaLog2e = 1.4426950408889634f;
+constexpr int kSaD = 128;          // head dim
+constexpr int kSaG = 16;           // query heads per kv head
+constexpr int kSaStageKeys = 16;   // keys per pipeline stage
+constexpr int kSaRing = 3;         // LDS ring depth (stages)
+constexpr int kSaStageBytes = 2 * kSaStageKeys * kSaD * 2;  // K + V rows: 8 KiB
+constexpr int kSaMaxEntries = 4096;                         // K*64, K <= 64
+constexpr float kSaRescale = 8.f;  // lazy-rescale threshold (log2 units)
+
+// 256 zero bytes: the K and V "row" of every entry that is not attended, so
+// each stage issues the same loads (masked keys then score 0 and carry P = 0
+// against a V of zeros).
+__device__ __align__(256) uint32_t sa_zero_row[64];
+
+struct SaArgs {
+  const __bf16* q;
+  int64_t q_st, q_sh;
+  const char* kc;
+  const char* vc;
+  int64_t row_bytes;   // bytes between consecutive cache rows
+  int64_t n_rows;      // rows of the cache viewed as [-1, D]
+  const int32_t* idx;
+  int64_t i_sh, i_st, i_sk;
+  const int32_t* bt;   // [B, L] (fused slots), or null
+  int64_t bt_sb;
+  const int32_t* slots;  // [T, Hkv, K*64] slot table, or null
+  const int32_t* tok_bs;
+  const int32_t* pos;
+  const int32_t* slen;
+  int32_t pos_n, slen_n;
+  void* out;           // [T, Hkv*16, 128] contiguous
+  int32_t T, Hkv, K, B, L;
+  float c;             // softmax scale * log2(e)
+};
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* sa_lds_ptr;
+typedef __attribute__((address_space(3))) i16x4 sa_lds_i16x4;
+
+// Global-to-LDS load of 16 bytes per lane at `addr`, written at M0 + 16*lane.
+// Issued from inline assembly so that the compiler, which does not see it,
+// inserts no waits for it: the kernel waits itself with exact vmcnt counts
+// (every stage issues the same eight loads).  No immediate offset is used.
+__device__ __forceinline__ void sa_dma16(uint64_t addr, int m0) {
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(addr)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void sa_vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ int lds_addr(const void* p) {
+  return static_cast<int>(reinterpret_cast<uintptr_t>((sa_lds_ptr)(p)));
+}
+
+// The key this lane gathers in every stage: lane l loads, in load i, the
+// 16-byte chunk 4i + l/16 of key (l%16) ^ (4 * ((l/16) & 1)).  The XOR keeps
+// the transposing V reads free of bank conflicts; the K fragment reads stay
+// one 16-byte chunk per lane.
+__device__ __forceinline__ int sa_lane_key(int lane) { return (lane & 15) ^ (4 * ((lane >> 4) & 1)); }
+
+// Issue the eight loads of stage `sg` into ring buffer `buf`: the K rows
+// (bytes 0..4095) and V rows (4096..8191).  Chunk c of key k lands at byte
+// 1024*(c/4) + 16*(16*(c%4) + (k ^ 4*((c%4)&1))) of each half.
+__device__ __forceinline__ void sa_issue(const SaArgs& a, const int32_t* srow, int sg, char* buf) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t row = srow[kSaStageKeys * sg + sa_lane_key(lane)];
+  const uint64_t col = static_cast<uint64_t>(16 * (lane >> 4));
+  uint64_t ka, va;
+  if (row >= 0) {
+    const uint64_t off = static_cast<uint64_t>(row) * static_cast<uint64_t>(a.row_bytes) + col;
+    ka = reinterpret_cast<uint64_t>(a.kc) + off;
+    va = reinterpret_cast<uint64_t>(a.vc) + off;
+  } else {
+    ka = va = reinterpret_cast<uint64_t>(sa_zero_row) + col;
+  }
+  const int m0 = __builtin_amdgcn_readfirstlane(lds_addr(buf));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sa_dma16(ka + 64 * i, m0 + 1024 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sa_dma16(va + 64 * i, m0 + 4096 + 1024 * i);
+}
+
+// Wait until the loads of the stage about to be computed have landed: the
+// stages issued after it (0 .. kRing-1) leave 8 loads each outstanding.
+__device__ __forceinline__ void sa_wait_stage(int issued_after) {
+  if (issued_after >= 2)
+    sa_vm_wait<16>();
+  else if (issued_after == 1)
+    sa_vm_wait<8>();
+  else
+    sa_vm_wait<0>();
+}
+
+// The stages to compute: a 256-bit mask in four scalar words (separate
+// variables, not an array, so that no index into it is a runtime value).
+struct SaStages {
+  uint64_t w0, w1, w2, w3;
+};
+
+// Lowest set stage of the mask (-1 if none); clears it.
+__device__ __forceinline__ int sa_pop(SaStages& m) {
+  if (m.w0) { const int b = __builtin_ctzll(m.w0); m.w0 &= m.w0 - 1; return b; }
+  if (m.w1) { const int b = __builtin_ctzll(m.w1); m.w1 &= m.w1 - 1; return 64 + b; }
+  if (m.w2) { const int b = __builtin_ctzll(m.w2); m.w2 &= m.w2 - 1; return 128 + b; }
+  if (m.w3) { const int b = __builtin_ctzll(m.w3); m.w3 &= m.w3 - 1; return 192 + b; }
+  return -1;
+}
+
+template <typename OutT>
+__device__ __forceinline__ void sa_store4(OutT* p, f32x4 v);
+template <>
+__device__ __forceinline__ void sa_store4<float>(float* p, f32x4 v) {
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+template <>
+__device__ __forceinline__ void sa_store4<uint16_t>(uint16_t* p, f32x4 v) {
+  const uint32_t lo = f32_to_bf16_bits(v.x) | (static_cast<uint32_t>(f32_to_bf16_bits(v.y)) << 16);
+  const uint32_t hi = f32_to_bf16_bits(v.z) | (static_cast<uint32_t>(f32_to_bf16_bits(v.w)) << 16);
+  *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+template <typename OutT, bool kTable>
+__global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
+  __shared__ int32_t srow[kSaMaxEntries];                         // 16 KiB
+  __shared__ __align__(16) char ring[kSaRing][kSaStageBytes];     // 24 KiB
+  const int lane = threadIdx.x;
+  const int t = blockIdx.x, h = blockIdx.y;
+  const int n_entries = a.K * 64;
+
+  const int32_t b = a.tok_bs[t];
+  const bool tok_ok = b >= 0 && b < a.B;
+  int32_t lim = 0;
+  if (tok_ok) {
+    const int32_t sl = a.slen[a.slen_n == 1 ? 0 : b];
+    const int32_t ps = a.pos[a.pos_n == 1 ? 0 : t];
+    lim = sl < ps ? sl : ps;
+  }
+
+  // ---- phase 1: the row of every entry (or -1), and the stages to compute
+  SaStages stages{0, 0, 0, 0};
+  const int32_t* idx_t = a.idx + static_cast<int64_t>(h) * a.i_sh + static_cast<int64_t>(t) * a.i_st;
+  const int32_t* slot_t =
+      kTable ? a.slots + (static_cast<int64_t>(t) * a.Hkv + h) * n_entries : nullptr;
+  for (int k = 0; k < a.K; ++k) {
+    const int32_t id = idx_t[static_cast<int64_t>(k) * a.i_sk];  // wave-uniform
+    const int32_t p = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(lane));
+    bool ok = tok_ok && p >= 0 && p < lim;
+    int32_t row = -1;
+    if (ok) {
+      if constexpr (kTable) {
+        row = slot_t[64 * k + lane];
+      } else {
+        const int32_t pc = p < a.L - 1 ? p : a.L - 1;
+        const int32_t v = a.bt[static_cast<int64_t>(b) * a.bt_sb + pc];
+        row = static_cast<int32_t>(static_cast<uint32_t>(a.Hkv) * static_cast<uint32_t>(v) +
+                                   static_cast<uint32_t>(h));
+      }
+      ok = row >= 0 && row < a.n_rows;
+    }
+    srow[64 * k + lane] = ok ? row : -1;
+    // Block k holds stages 4k .. 4k+3: bit q4 of its nibble marks a stage
+    // with an attended entry.
+    const uint64_t m = __ballot(ok);
+    uint64_t nib = 0;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) nib |= ((m >> (16 * q4)) & 0xFFFFull) ? (1ull << q4) : 0ull;
+    nib <<= 4 * (k & 15);
+    const int w = k >> 4;  // wave-uniform
+    stages.w0 |= w == 0 ? nib : 0ull;
+    stages.w1 |= w == 1 ? nib : 0ull;
+    stages.w2 |= w == 2 ? nib : 0ull;
+    stages.w3 |= w == 3 ? nib : 0ull;
+  }
+
+  // Query fragments, the B operand of S^T = K Q^T: lane (head n, g) holds
+  // q[t, 16h + n, 32cc + 8g .. +8].
+  bf16x8 qf[4];
+  {
+    const __bf16* qp = a.q + static_cast<int64_t>(t) * a.q_st +
+                       static_cast<int64_t>(kSaG * h + (lane & 15)) * a.q_sh + 8 * (lane >> 4);
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const bf16x8*>(qp + 32 * cc);
+  }
+  // The compiler's own loads (the queries, phase 1) complete here, before the
+  // ring's loads are issued: it does not count those, and a wait of its own
+  // placed inside the loop would drain the ring on every stage.
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) asm volatile("" : : "v"(qf[cc]));
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+
+  // ---- phase 2: the pipelined stages.  fifo[0..2] are the stages in flight,
+  // oldest first; the oldest is in ring buffer `slot`, the next ones follow
+  // cyclically.
+  static_assert(kSaRing == 3, "the stage FIFO below holds three stages");
+  int fifo0 = sa_pop(stages), fifo1 = sa_pop(stages), fifo2 = sa_pop(stages);
+  if (fifo0 >= 0) sa_issue(a, srow, fifo0, ring[0]);
+  if (fifo1 >= 0) sa_issue(a, srow, fifo1, ring[1]);
+  if (fifo2 >= 0) sa_issue(a, srow, fifo2, ring[2]);
+  // Per-lane constants of the stage computation.
+  const int g = lane >> 4;
+  const int kread = 16 * (lane ^ (4 * ((lane >> 4) & 1)));  // K fragment: chunk 4cc+g of key lane%16
+  // V^T fragment (dims 16dt + 4(s%4) .. +3 of key 4g + s/4, s = lane%16):
+  // byte 1024*(dt/2) + 512*(dt%2) + vread of the V half.
+  const int s = lane & 15;
+  const int vkey = 4 * g + (s >> 2);
+  const int vbit = (s >> 1) & 1;
+  const int vread = 256 * vbit + 16 * (vkey ^ (4 * vbit)) + 8 * (s & 1);
+
+  float m_run = -INFINITY;  // c * running max of this lane's head
+  float l_run = 0.f;        // sum of exp2 against it over this lane's keys
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const float c = a.c;
+  int slot = 0;
+  while (fifo0 >= 0) {
+    const int sg = fifo0;
+    sa_wait_stage((fifo1 >= 0 ? 1 : 0) + (fifo2 >= 0 ? 1 : 0));
+    const char* buf = ring[slot];
+
+    // scores S^T (keys 4g + r of the stage, head lane%16)
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(buf + 1024 * cc + kread);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[cc], acc, 0, 0, 0);
+    }
+    // keys of the stage not attended -> -inf
+    const int32_t* sr = srow + kSaStageKeys * sg + 4 * g;
+    const i32x4 rv = *reinterpret_cast<const i32x4*>(sr);
+    float x0 = rv.x >= 0 ? acc.x : -INFINITY;
+    float x1 = rv.y >= 0 ? acc.y : -INFINITY;
+    float x2 = rv.z >= 0 ? acc.z : -INFINITY;
+    float x3 = rv.w >= 0 ? acc.w : -INFINITY;
+    float mx = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mxc = mx * c;  // -inf when the head has no attended key in the stage
+    if (__ballot(mxc > m_run + kSaRescale) != 0) {
+      const float m_new = fmaxf(m_run, mxc);
+      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        o[dt].x *= alpha;
+        o[dt].y *= alpha;
+        o[dt].z *= alpha;
+        o[dt].w *= alpha;
+      }
+      m_run = m_new;
+    }
+    // exponentials (0 for -inf scores; m_run is finite once a key was seen)
+    const float mr = m_run == -INFINITY ? 0.f : m_run;
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, c, -mr));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, c, -mr));
+    const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(x2, c, -mr));
+    const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(x3, c, -mr));
+    l_run += (p0 + p1) + (p2 + p3);
+    const i16x4 pb = {static_cast<short>(f32_to_bf16_bits(p0)), static_cast<short>(f32_to_bf16_bits(p1)),
+                      static_cast<short>(f32_to_bf16_bits(p2)), static_cast<short>(f32_to_bf16_bits(p3))};
+    // O^T += V^T P^T, one 16-dim tile at a time
+    sa_lds_i16x4* vb = (sa_lds_i16x4*)(buf + 4096 + vread);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const i16x4 vf = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (sa_lds_i16x4*)((__attribute__((address_space(3))) char*)vb + 1024 * (dt >> 1) + 512 * (dt & 1)));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pb, o[dt], 0, 0, 0);
+    }
+    // Refill this ring buffer with the next stage (its reads are done: the
+    // MFMAs above consumed them).
+    const int nsg = sa_pop(stages);
+    if (nsg >= 0) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      sa_issue(a, srow, nsg, ring[slot]);
+    }
+    fifo0 = fifo1;
+    fifo1 = fifo2;
+    fifo2 = nsg;
+    slot = slot == kSaRing - 1 ? 0 : slot + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- normalise and store: lane (head n, g) holds dims 16dt + 4g + r
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  OutT* orow = static_cast<OutT*>(a.out) +
+               (static_cast<int64_t>(t) * a.Hkv * kSaG + kSaG * h + (lane & 15)) * kSaD + 4 * g;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    f32x4 v = o[dt];
+    v.x *= inv;
+    v.y *= inv;
+    v.z *= inv;
+    v.w *= inv;
+    sa_store4<OutT>(orow + 16 * dt, v);
+  }
+}
+
+}  // namespace
+}  // namespace unum
+
+extern "C" int unum_sparse_paged_attention(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* key_cache,
+    const void* value_cache, int64_t kv_row_stride, int64_t n_rows, const int32_t* topk_idx,
+    int64_t topk_stride_h, int64_t topk_stride_t, int64_t topk_stride_k,
+    const int32_t* block_table, int64_t bt_stride_b, const int32_t* slots,
+    const int32_t* token_to_bs, const int32_t* token_pos_in_bs, int64_t pos_numel,
+    const int32_t* seqlen_q, int64_t seqlen_numel, void* out, int32_t out_dtype, int64_t T,
+    int64_t Hq, int64_t Hkv, int64_t D, int64_t K, int64_t B, int64_t L, float scale,
+    void* stream) {
+  using namespace unum;
+  clear_error();
+  const char* op = "sparse_paged_attention";
+  UNUM_REQUIRE(T >= 0 && Hq > 0 && Hkv > 0 && D > 0 && K >= 0 && B >= 0 && L >= 0,
+               "%s: bad sizes (T=%lld Hq=%lld Hkv=%lld D=%lld K=%lld B=%lld L=%lld)", op,
+               (long long)T, (long long)Hq, (long long)Hkv, (long long)D, (long long)K,
+               (long long)B, (long long)L);
+  if (T == 0) return UNUM_OK;
+  if (Hq != kSaG * Hkv || D != kSaD)
+    UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "%s: needs 16 query heads per kv head and D = 128 (got Hq=%lld, "
+              "Hkv=%lld, D=%lld)", op, (long long)Hq, (long long)Hkv, (long long)D);
+  UNUM_REQUIRE(K <= kSaMaxEntries / 64, "%s: at most %d blocks per token (K=%lld)", op,
+               kSaMaxEntries / 64, (long long)K);
+  UNUM_REQUIRE(q && key_cache && value_cache && topk_idx && token_to_bs && token_pos_in_bs &&
+                   seqlen_q && out,
+               "%s: null pointer", op);
+  UNUM_REQUIRE(slots || (block_table && B >= 1 && L >= 1),
+               "%s: a block table (B, L >= 1) or a slot table is required", op);
+  UNUM_REQUIRE(pos_numel == 1 || pos_numel == T, "%s: token_pos_in_bs has %lld entries (T=%lld)",
+               op, (long long)pos_numel, (long long)T);
+  UNUM_REQUIRE(seqlen_numel == 1 || seqlen_numel >= B, "%s: seqlen_q has %lld entries (B=%lld)", op,
+               (long long)seqlen_numel, (long long)B);
+  UNUM_REQUIRE(n_rows >= 0 && kv_row_stride >= D && (kv_row_stride % 8) == 0,
+               "%s: cache rows must be D elements or more apart, in multiples of 8 (stride %lld)",
+               op, (long long)kv_row_stride);
+  UNUM_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (q_stride_t % 8) == 0 &&
+                   (q_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(key_cache) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(value_cache) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "%s: q, the caches and out must be 16-byte aligned", op);
+  UNUM_REQUIRE(T <= INT32_MAX && Hkv <= 65535 && n_rows <= INT32_MAX && B <= INT32_MAX &&
+                   L <= INT32_MAX,
+               "%s: size exceeds the kernel's index range", op);
+  SaArgs a{};
+  a.q = static_cast<const __bf16*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.kc = static_cast<const char*>(key_cache);
+  a.vc = static_cast<const char*>(value_cache);
+  a.row_bytes = kv_row_stride * 2;
+  a.n_rows = n_rows;
+  a.idx = topk_idx;
+  a.i_sh = topk_stride_h;
+  a.i_st = topk_stride_t;
+  a.i_sk = topk_stride_k;
+  a.bt = block_table;
+  a.bt_sb = bt_stride_b;
+  a.slots = slots;
+  a.tok_bs = token_to_bs;
+  a.pos = token_pos_in_bs;
+  a.slen = seqlen_q;
+  a.pos_n = static_cast<int32_t>(pos_numel);
+  a.slen_n = static_cast<int32_t>(seqlen_numel == 1 ? 1 : 2);
+  a.out = out;
+  a.T = static_cast<int32_t>(T);
+  a.Hkv = static_cast<int32_t>(Hkv);
+  a.K = static_cast<int32_t>(K);
+  a.B = static_cast<int32_t>(B);
+  a.L = static_cast<int32_t>(L);
+  a.c = scale * kSaLog2e;
+  const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(Hkv));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (out_dtype == UNUM_DTYPE_BF16) {
+    if (slots)
+      hipLaunchKernelGGL((sparse_attn_kernel<uint16_t, true>), grid, dim3(kWave), 0, s, a);
+    else
+      hipLaunchKernelGGL((sparse_attn_kernel<uint16_t, false>), grid, dim3(kWave), 0, s, a);
+  } else if (out_dtype == UNUM_DTYPE_F32) {
+    if (slots)
+      hipLaunchKernelGGL((sparse_attn_kernel<float, true>), grid, dim3(kWave), 0, s, a);
+    else
+      hipLaunchKernelGGL((sparse_attn_kernel<float, false>), grid, dim3(kWave), 0, s, a);
+  } else {
+    UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "%s: unsupported out dtype %d", op, out_dtype);
+  }
+  return check_launch(op);
+}
