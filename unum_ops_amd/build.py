@@ -43,6 +43,9 @@ HIP_FLAGS = [
 # accumulation registers.
 FILE_FLAGS = {
     "stage1.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # Stage 2 keeps its P.V accumulators across the whole loop; in the
+    # accumulation registers the compiler copied them out and back every stage.
+    "sparse_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -17,15 +17,16 @@
 //
 // One wave per (t, h).  Phase 1 stages the row of each of the K*64 entries
 // (or -1) in LDS and marks which 16-key stages hold an attended entry.
-// Phase 2 streams those stages through a ring of LDS buffers: each stage's
-// 16 K rows and 16 V rows (8 KiB) are gathered by buffer-free global-to-LDS
-// loads, issued kRing-1 stages ahead of the one being computed.  Per stage:
+// Phase 2 gathers each such stage's 16 K rows and 16 V rows (8 KiB) into
+// registers, kRing stages ahead of the one being computed (ordinary loads,
+// so the compiler's waits are exact).  Per stage:
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (keys as M, heads as N), so a
 //     lane holds four keys of one head: the online-softmax state (max, sum)
 //     is one head per lane and needs no transposes;
 //   * P^T (bf16) is, as it stands in the accumulator layout, the B operand of
-//     v_mfma_f32_16x16x16_bf16 for O^T += V^T P^T; V^T fragments come from the
-//     row-major V rows in LDS through ds_read_b64_tr_b16 (transposing reads);
+//     v_mfma_f32_16x16x16_bf16 for O^T += V^T P^T; the V rows go to a 4 KiB
+//     LDS buffer and come back as V^T fragments through ds_read_b64_tr_b16
+//     (transposing reads);
 //   * the running max moves only when a stage's max exceeds it by more than
 //     8 (log2 units), so the O^T rescale is rare; exponentials stay <= 2^8.
 #include "common.h"
@@ -37,8 +38,10 @@ constexpr float kSaLog2e = 1.4426950408889634f;
 constexpr int kSaD = 128;          // head dim
 constexpr int kSaG = 16;           // query heads per kv head
 constexpr int kSaStageKeys = 16;   // keys per pipeline stage
-constexpr int kSaRing = 3;         // LDS ring depth (stages)
-constexpr int kSaStageBytes = 2 * kSaStageKeys * kSaD * 2;  // K + V rows: 8 KiB
+// Stages gathered ahead (register sets of 32 VGPRs).  Two, three and four
+// measured the same on the cfg4 and cfg5 selections (351 / 1840 us); six,
+// at one wave per SIMD, measured slower on cfg4 (620 against 422 us).
+constexpr int kSaRing = 3;
 constexpr int kSaMaxEntries = 4096;                         // K*64, K <= 64
 constexpr float kSaRescale = 8.f;  // lazy-rescale threshold (log2 units)
 
@@ -72,18 +75,38 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* sa_lds_ptr;
 typedef __attribute__((address_space(3))) i16x4 sa_lds_i16x4;
 
-// Global-to-LDS load of 16 bytes per lane at `addr`, written at M0 + 16*lane.
-// Issued from inline assembly so that the compiler, which does not see it,
-// inserts no waits for it: the kernel waits itself with exact vmcnt counts
-// (every stage issues the same eight loads).  No immediate offset is used.
-__device__ __forceinline__ void sa_dma16(uint64_t addr, int m0) {
+// Global-to-LDS load of 4 bytes per lane at `addr` (a 256-byte run per
+// instruction), written at M0 + 4*lane.  Issued from inline assembly so that
+// the compiler inserts no wait per load: all of them are in flight at once
+// and the kernel waits once, with vmcnt(0).
+__device__ __forceinline__ void sa_dma4(uint64_t addr, int m0) {
   int saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
       : "s"(m0), "v"(addr)
       : "memory");
+}
+
+// Max / sum of v over the lanes l and l^16 (l^32): v_permlane16_swap
+// (v_permlane32_swap) with v in both operands returns each lane's value and
+// its partner's, one in each result.
+__device__ __forceinline__ float sa_max_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sa_max_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sa_sum_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sa_sum_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 template <int N>
@@ -96,43 +119,39 @@ __device__ __forceinline__ int lds_addr(const void* p) {
   return static_cast<int>(reinterpret_cast<uintptr_t>((sa_lds_ptr)(p)));
 }
 
-// The key this lane gathers in every stage: lane l loads, in load i, the
-// 16-byte chunk 4i + l/16 of key (l%16) ^ (4 * ((l/16) & 1)).  The XOR keeps
-// the transposing V reads free of bank conflicts; the K fragment reads stay
-// one 16-byte chunk per lane.
-__device__ __forceinline__ int sa_lane_key(int lane) { return (lane & 15) ^ (4 * ((lane >> 4) & 1)); }
+// A stage in flight: this lane's K and V chunks of its key (lane l gathers
+// key l%16, 16-byte chunks 4i + l/16, i < 4 -- for K exactly the A operand
+// of the score MFMA, chunk 4cc + g of key m) and the stage's mask of
+// attended keys (bit j: key j; lanes 0..15 gather keys 0..15).
+struct SaStage {
+  bf16x8 k[4];
+  bf16x8 v[4];
+  uint32_t mask;
+};
 
-// Issue the eight loads of stage `sg` into ring buffer `buf`: the K rows
-// (bytes 0..4095) and V rows (4096..8191).  Chunk c of key k lands at byte
-// 1024*(c/4) + 16*(16*(c%4) + (k ^ 4*((c%4)&1))) of each half.
-__device__ __forceinline__ void sa_issue(const SaArgs& a, const int32_t* srow, int sg, char* buf) {
+// Issue the gathers of stage `sg` (ordinary loads: the compiler waits for
+// each stage's loads exactly where they are used).  A key that is not
+// attended gathers the zero row, and so does every key when sg < 0 (no
+// stage left): every call issues the same eight loads, so on every path
+// through the ring the same number of loads follows each set and the
+// compiler's wait before using a set stays a partial one.
+__device__ __forceinline__ void sa_issue(const SaArgs& a, const int32_t* srow, int sg, SaStage& st) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int32_t row = srow[kSaStageKeys * sg + sa_lane_key(lane)];
+  const int32_t row = sg >= 0 ? srow[kSaStageKeys * sg + (lane & 15)] : -1;
   const uint64_t col = static_cast<uint64_t>(16 * (lane >> 4));
-  uint64_t ka, va;
+  const char *kp, *vp;
   if (row >= 0) {
     const uint64_t off = static_cast<uint64_t>(row) * static_cast<uint64_t>(a.row_bytes) + col;
-    ka = reinterpret_cast<uint64_t>(a.kc) + off;
-    va = reinterpret_cast<uint64_t>(a.vc) + off;
+    kp = a.kc + off;
+    vp = a.vc + off;
   } else {
-    ka = va = reinterpret_cast<uint64_t>(sa_zero_row) + col;
+    kp = vp = reinterpret_cast<const char*>(sa_zero_row) + col;
   }
-  const int m0 = __builtin_amdgcn_readfirstlane(lds_addr(buf));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sa_dma16(ka + 64 * i, m0 + 1024 * i);
+  for (int i = 0; i < 4; ++i) st.k[i] = *reinterpret_cast<const bf16x8*>(kp + 64 * i);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sa_dma16(va + 64 * i, m0 + 4096 + 1024 * i);
-}
-
-// Wait until the loads of the stage about to be computed have landed: the
-// stages issued after it (0 .. kRing-1) leave 8 loads each outstanding.
-__device__ __forceinline__ void sa_wait_stage(int issued_after) {
-  if (issued_after >= 2)
-    sa_vm_wait<16>();
-  else if (issued_after == 1)
-    sa_vm_wait<8>();
-  else
-    sa_vm_wait<0>();
+  for (int i = 0; i < 4; ++i) st.v[i] = *reinterpret_cast<const bf16x8*>(vp + 64 * i);
+  st.mask = static_cast<uint32_t>(__ballot(row >= 0) & 0xFFFFull);
 }
 
 // The stages to compute: a 256-bit mask in four scalar words (separate
@@ -163,10 +182,10 @@ __device__ __forceinline__ void sa_store4<uint16_t>(uint16_t* p, f32x4 v) {
   *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
 }
 
-template <typename OutT, bool kTable>
+template <typename OutT, bool kTable, int kRing>
 __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
   __shared__ int32_t srow[kSaMaxEntries];                         // 16 KiB
-  __shared__ __align__(16) char ring[kSaRing][kSaStageBytes];     // 24 KiB
+  __shared__ __align__(16) char vst[kSaStageKeys * kSaD * 2];     // 4 KiB: a stage's V rows
   const int lane = threadIdx.x;
   const int t = blockIdx.x, h = blockIdx.y;
   const int n_entries = a.K * 64;
@@ -180,40 +199,57 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
     lim = sl < ps ? sl : ps;
   }
 
-  // ---- phase 1: the row of every entry (or -1), and the stages to compute
+  // ---- phase 1: the row of every entry (or -1), and the stages to compute.
+  // The 64 table values of each block -- slot-table entries, or the block
+  // table's entries at the block's positions (clamped into the row; the
+  // clamp only matters for entries that are not attended or at p >= L) --
+  // are gathered into srow by global-to-LDS loads, all in flight at once,
+  // then turned into rows in place.
   SaStages stages{0, 0, 0, 0};
   const int32_t* idx_t = a.idx + static_cast<int64_t>(h) * a.i_sh + static_cast<int64_t>(t) * a.i_st;
-  const int32_t* slot_t =
-      kTable ? a.slots + (static_cast<int64_t>(t) * a.Hkv + h) * n_entries : nullptr;
-  for (int k = 0; k < a.K; ++k) {
-    const int32_t id = idx_t[static_cast<int64_t>(k) * a.i_sk];  // wave-uniform
-    const int32_t p = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(lane));
-    bool ok = tok_ok && p >= 0 && p < lim;
-    int32_t row = -1;
-    if (ok) {
-      if constexpr (kTable) {
-        row = slot_t[64 * k + lane];
-      } else {
-        const int32_t pc = p < a.L - 1 ? p : a.L - 1;
-        const int32_t v = a.bt[static_cast<int64_t>(b) * a.bt_sb + pc];
-        row = static_cast<int32_t>(static_cast<uint32_t>(a.Hkv) * static_cast<uint32_t>(v) +
-                                   static_cast<uint32_t>(h));
+  const int srow_m0 = __builtin_amdgcn_readfirstlane(lds_addr(srow));
+  // Lane k holds block id k: one load, complete before the gathers below are
+  // issued (a load of the compiler's inside their loop would make it wait
+  // for every gather issued before it).
+  int32_t lane_id = lane < a.K ? idx_t[static_cast<int64_t>(lane) * a.i_sk] : -1;
+  asm volatile("" : "+v"(lane_id));
+  if (tok_ok) {
+    if constexpr (kTable) {
+      const int32_t* src = a.slots + (static_cast<int64_t>(t) * a.Hkv + h) * n_entries + lane;
+      for (int k = 0; k < a.K; ++k)
+        sa_dma4(reinterpret_cast<uint64_t>(src + 64 * k), srow_m0 + 256 * k);
+    } else {
+      const int32_t* btr = a.bt + static_cast<int64_t>(b) * a.bt_sb;
+      for (int k = 0; k < a.K; ++k) {
+        const int32_t id = __builtin_amdgcn_readlane(lane_id, k);
+        int32_t pc = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(lane));
+        pc = pc < 0 ? 0 : (pc > a.L - 1 ? a.L - 1 : pc);
+        sa_dma4(reinterpret_cast<uint64_t>(btr + pc), srow_m0 + 256 * k);
       }
-      ok = row >= 0 && row < a.n_rows;
     }
-    srow[64 * k + lane] = ok ? row : -1;
-    // Block k holds stages 4k .. 4k+3: bit q4 of its nibble marks a stage
-    // with an attended entry.
-    const uint64_t m = __ballot(ok);
-    uint64_t nib = 0;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int k = 0; k < a.K; ++k) {
+      const int32_t id = __builtin_amdgcn_readlane(lane_id, k);
+      const int32_t p = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(lane));
+      const int32_t v = srow[64 * k + lane];
+      const int32_t row = kTable ? v
+                                 : static_cast<int32_t>(static_cast<uint32_t>(a.Hkv) * static_cast<uint32_t>(v) +
+                                                        static_cast<uint32_t>(h));
+      const bool ok = p >= 0 && p < lim && row >= 0 && row < a.n_rows;
+      srow[64 * k + lane] = ok ? row : -1;
+      // Block k holds stages 4k .. 4k+3: bit q4 of its nibble marks a stage
+      // with an attended entry.
+      const uint64_t m = __ballot(ok);
+      uint64_t nib = 0;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) nib |= ((m >> (16 * q4)) & 0xFFFFull) ? (1ull << q4) : 0ull;
-    nib <<= 4 * (k & 15);
-    const int w = k >> 4;  // wave-uniform
-    stages.w0 |= w == 0 ? nib : 0ull;
-    stages.w1 |= w == 1 ? nib : 0ull;
-    stages.w2 |= w == 2 ? nib : 0ull;
-    stages.w3 |= w == 3 ? nib : 0ull;
+      for (int q4 = 0; q4 < 4; ++q4) nib |= ((m >> (16 * q4)) & 0xFFFFull) ? (1ull << q4) : 0ull;
+      nib <<= 4 * (k & 15);
+      const int w = k >> 4;  // wave-uniform
+      stages.w0 |= w == 0 ? nib : 0ull;
+      stages.w1 |= w == 1 ? nib : 0ull;
+      stages.w2 |= w == 2 ? nib : 0ull;
+      stages.w3 |= w == 3 ? nib : 0ull;
+    }
   }
 
   // Query fragments, the B operand of S^T = K Q^T: lane (head n, g) holds
@@ -235,16 +271,14 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
   // ---- phase 2: the pipelined stages.  fifo[0..2] are the stages in flight,
   // oldest first; the oldest is in ring buffer `slot`, the next ones follow
   // cyclically.
-  static_assert(kSaRing == 3, "the stage FIFO below holds three stages");
-  int fifo0 = sa_pop(stages), fifo1 = sa_pop(stages), fifo2 = sa_pop(stages);
-  if (fifo0 >= 0) sa_issue(a, srow, fifo0, ring[0]);
-  if (fifo1 >= 0) sa_issue(a, srow, fifo1, ring[1]);
-  if (fifo2 >= 0) sa_issue(a, srow, fifo2, ring[2]);
   // Per-lane constants of the stage computation.
   const int g = lane >> 4;
-  const int kread = 16 * (lane ^ (4 * ((lane >> 4) & 1)));  // K fragment: chunk 4cc+g of key lane%16
+  // V chunk i of this lane's key goes to byte 1024*i + vput of vst, which
+  // puts chunk c of key k at 1024*(c/4) + 16*(16*(c%4) + (k ^ 4*((c%4)&1))):
+  // the transposing reads below then hit no bank twice.
+  const int vput = 16 * (lane ^ (4 * (g & 1)));
   // V^T fragment (dims 16dt + 4(s%4) .. +3 of key 4g + s/4, s = lane%16):
-  // byte 1024*(dt/2) + 512*(dt%2) + vread of the V half.
+  // byte 1024*(dt/2) + 512*(dt%2) + vread of vst.
   const int s = lane & 15;
   const int vkey = 4 * g + (s >> 2);
   const int vbit = (s >> 1) & 1;
@@ -255,32 +289,27 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
   f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   const float c = a.c;
-  int slot = 0;
-  while (fifo0 >= 0) {
-    const int sg = fifo0;
-    sa_wait_stage((fifo1 >= 0 ? 1 : 0) + (fifo2 >= 0 ? 1 : 0));
-    const char* buf = ring[slot];
 
+  auto compute = [&](const SaStage& st) {
+    // V rows to LDS for the transposing reads
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<bf16x8*>(vst + 1024 * i + vput) = st.v[i];
     // scores S^T (keys 4g + r of the stage, head lane%16)
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(buf + 1024 * cc + kread);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[cc], acc, 0, 0, 0);
+    for (int cc = 0; cc < 4; ++cc) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.k[cc], qf[cc], acc, 0, 0, 0);
+    float x0 = acc.x, x1 = acc.y, x2 = acc.z, x3 = acc.w;
+    if (st.mask != 0xFFFFu) {  // keys of the stage not attended -> -inf (wave-uniform test)
+      const uint32_t mb = st.mask >> (4 * g);
+      x0 = (mb & 1u) ? x0 : -INFINITY;
+      x1 = (mb & 2u) ? x1 : -INFINITY;
+      x2 = (mb & 4u) ? x2 : -INFINITY;
+      x3 = (mb & 8u) ? x3 : -INFINITY;
     }
-    // keys of the stage not attended -> -inf
-    const int32_t* sr = srow + kSaStageKeys * sg + 4 * g;
-    const i32x4 rv = *reinterpret_cast<const i32x4*>(sr);
-    float x0 = rv.x >= 0 ? acc.x : -INFINITY;
-    float x1 = rv.y >= 0 ? acc.y : -INFINITY;
-    float x2 = rv.z >= 0 ? acc.z : -INFINITY;
-    float x3 = rv.w >= 0 ? acc.w : -INFINITY;
     float mx = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mxc = mx * c;  // -inf when the head has no attended key in the stage
+    mx = sa_max_x32(sa_max_x16(mx));
+    const float mxc = mx * c;  // every head has an attended key in the stage
     if (__ballot(mxc > m_run + kSaRescale) != 0) {
       const float m_new = fmaxf(m_run, mxc);
       const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -294,40 +323,49 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
       }
       m_run = m_new;
     }
-    // exponentials (0 for -inf scores; m_run is finite once a key was seen)
-    const float mr = m_run == -INFINITY ? 0.f : m_run;
-    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, c, -mr));
-    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, c, -mr));
-    const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(x2, c, -mr));
-    const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(x3, c, -mr));
+    // exponentials (0 for -inf scores); m_run is finite after the first stage
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, c, -m_run));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, c, -m_run));
+    const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(x2, c, -m_run));
+    const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(x3, c, -m_run));
     l_run += (p0 + p1) + (p2 + p3);
     const i16x4 pb = {static_cast<short>(f32_to_bf16_bits(p0)), static_cast<short>(f32_to_bf16_bits(p1)),
                       static_cast<short>(f32_to_bf16_bits(p2)), static_cast<short>(f32_to_bf16_bits(p3))};
     // O^T += V^T P^T, one 16-dim tile at a time
-    sa_lds_i16x4* vb = (sa_lds_i16x4*)(buf + 4096 + vread);
+    sa_lds_i16x4* vb = (sa_lds_i16x4*)(vst + vread);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const i16x4 vf = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (sa_lds_i16x4*)((__attribute__((address_space(3))) char*)vb + 1024 * (dt >> 1) + 512 * (dt & 1)));
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pb, o[dt], 0, 0, 0);
     }
-    // Refill this ring buffer with the next stage (its reads are done: the
-    // MFMAs above consumed them).
-    const int nsg = sa_pop(stages);
-    if (nsg >= 0) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      sa_issue(a, srow, nsg, ring[slot]);
-    }
-    fifo0 = fifo1;
-    fifo1 = fifo2;
-    fifo2 = nsg;
-    slot = slot == kSaRing - 1 ? 0 : slot + 1;
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
 
+  // ---- phase 2: the stages, gathered kRing ahead into a ring of register
+  // sets (indices known at compile time: the loop over the ring is
+  // unrolled); the ring is walked in order and so are the stages, so the
+  // first set left empty ends the walk.
+  SaStage r[kRing];
+  int sr[kRing];
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    sr[j] = sa_pop(stages);
+    sa_issue(a, srow, sr[j], r[j]);
+  }
+  for (bool more = true; more;) {
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) {
+      if (more && sr[j] >= 0) {
+        compute(r[j]);
+        sr[j] = sa_pop(stages);
+        sa_issue(a, srow, sr[j], r[j]);
+      } else {
+        more = false;
+      }
+    }
+  }
   // ---- normalise and store: lane (head n, g) holds dims 16dt + 4g + r
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  const float l_tot = sa_sum_x32(sa_sum_x16(l_run));
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   OutT* orow = static_cast<OutT*>(a.out) +
                (static_cast<int64_t>(t) * a.Hkv * kSaG + kSaG * h + (lane & 15)) * kSaD + 4 * g;
@@ -414,20 +452,23 @@ extern "C" int unum_sparse_paged_attention(
   a.B = static_cast<int32_t>(B);
   a.L = static_cast<int32_t>(L);
   a.c = scale * kSaLog2e;
+  UNUM_REQUIRE(out_dtype == UNUM_DTYPE_BF16 || out_dtype == UNUM_DTYPE_F32,
+               "%s: unsupported out dtype %d", op, out_dtype);
   const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(Hkv));
   hipStream_t s = static_cast<hipStream_t>(stream);
+#define UNUM_SA_LAUNCH(OutT, kTab) \
+  hipLaunchKernelGGL((sparse_attn_kernel<OutT, kTab, kSaRing>), grid, dim3(kWave), 0, s, a)
   if (out_dtype == UNUM_DTYPE_BF16) {
     if (slots)
-      hipLaunchKernelGGL((sparse_attn_kernel<uint16_t, true>), grid, dim3(kWave), 0, s, a);
+      UNUM_SA_LAUNCH(uint16_t, true);
     else
-      hipLaunchKernelGGL((sparse_attn_kernel<uint16_t, false>), grid, dim3(kWave), 0, s, a);
-  } else if (out_dtype == UNUM_DTYPE_F32) {
-    if (slots)
-      hipLaunchKernelGGL((sparse_attn_kernel<float, true>), grid, dim3(kWave), 0, s, a);
-    else
-      hipLaunchKernelGGL((sparse_attn_kernel<float, false>), grid, dim3(kWave), 0, s, a);
+      UNUM_SA_LAUNCH(uint16_t, false);
   } else {
-    UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "%s: unsupported out dtype %d", op, out_dtype);
+    if (slots)
+      UNUM_SA_LAUNCH(float, true);
+    else
+      UNUM_SA_LAUNCH(float, false);
   }
+#undef UNUM_SA_LAUNCH
   return check_launch(op);
 }
