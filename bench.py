@@ -481,8 +481,7 @@ def main():
             comps[name] = dict(us=per_op[name] * 1e3, tflops=flop / t / 1e12,
                                pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
                                config=f"{src} fused with the max-pool: pooled fp32 "
-                                      "[Hkv, Tq, NB] only (scores not stored); rows of at "
-                                      "most 512 keys (cfg3) run the two kernels")
+                                      "[Hkv, Tq, NB] only (scores not stored)")
     if "compress_keys_cfg5" in per_op:
         nbytes = 2 * 135168 * 2 * 128 + 2 * 8447 * 2 * 128
         t = per_op["compress_keys_cfg5"] * 1e-3

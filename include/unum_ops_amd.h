@@ -150,11 +150,11 @@ int unum_infllmv2_attn_stage1_noalloc(const void* q, int64_t q_stride_t, int64_t
  *   workspace / workspace_bytes  as unum_infllmv2_attn_stage1 (size from
  *          unum_infllmv2_attn_stage1_workspace_size): with it, rows over 512
  *          keys run the key-split kernels, pooling in their second pass;
- *          NULL runs whole rows.
+ *          NULL runs whole rows.  Rows of at most 512 keys need none.
  * Other arguments as unum_infllmv2_attn_stage1 and unum_max_pooling_1d_varlen.
- * Fused only on the key-streaming MFMA path: G = 16, D = 128, 16-byte
- * aligned q/k, scale > 0 and out_cols > 512.  Every other problem --
- * including rows of at most 512 keys -- returns UNUM_ERR_UNSUPPORTED; run
+ * Fused on the MFMA paths (G = 16, D = 128, 16-byte aligned q/k, scale > 0):
+ * rows of at most 512 keys pool in the LDS-resident kernel, longer rows in
+ * the key-streaming kernels.  Other shapes return UNUM_ERR_UNSUPPORTED; run
  * unum_infllmv2_attn_stage1 and unum_max_pooling_1d_varlen there.
  */
 int unum_infllmv2_attn_stage1_maxpool(const void* q, int64_t q_stride_t, int64_t q_stride_h,

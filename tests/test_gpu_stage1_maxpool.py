@@ -1,5 +1,6 @@
 """GPU parity of the fused stage-1 + max-pool entry point (fused in the
-K-streaming kernel for rows over 512 keys; shorter rows run the two ops).
+LDS-resident kernel for rows of at most 512 keys, in the K-streaming kernels
+for longer rows).
 
 The pooled scores must equal, bit for bit, the max-pool the oracle computes
 from the scores the same kernel wrote (``return_scores``), and the scores must
@@ -55,7 +56,8 @@ def test_lds_path_cfg3_slice(dev):
 def test_pool_width_vs_score_width(ctx, ctx_extra, dev):
     # max_context_len at or above the keys' span: pooled blocks past the
     # computed columns (the tail) hold at most the carried last tap.  8200
-    # tokens (511 keys) take the unfused pair, 9000 (561) the fused kernel.
+    # tokens (511 keys) take the LDS-resident kernel, 9000 (561) the
+    # streaming one; ctx_extra 2000 puts pooled blocks past the score row.
     d = workloads.stage1_inputs([40, 17], [2000, ctx], seed=33)
     _check(d, dev, ctx + ctx_extra)
 

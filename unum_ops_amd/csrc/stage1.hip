@@ -123,8 +123,8 @@ __device__ __forceinline__ void store_out<uint16_t>(uint16_t* p, float v) {
 
 // Zero [from, out_cols) of a row; lanes write consecutive elements.
 template <typename OutT>
-__device__ __forceinline__ void zero_tail(OutT* orow, int64_t from, int64_t out_cols) {
-  const int lane = threadIdx.x & (kWave - 1);
+__device__ __forceinline__ void zero_tail(OutT* orow, int64_t from, int64_t out_cols,
+                                          int lane = threadIdx.x & (kWave - 1)) {
   for (int64_t j = from + lane; j < out_cols; j += kWave) store_out<OutT>(orow + j, 0.f);
 }
 
@@ -179,8 +179,8 @@ __device__ __forceinline__ void buffer_store_out(__amdgpu_buffer_rsrc_t r, int o
 // block i (nothing is stored when `drop`); `carry` becomes this quad's last tap.
 __device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_rsrc_t prs,
                                           int32_t key0, int32_t lk, int32_t ob, float o,
-                                          float& carry, bool drop) {
-  const int lane = threadIdx.x & (kWave - 1);
+                                          float& carry, bool drop,
+                                          int lane = threadIdx.x & (kWave - 1)) {
   const float x = key0 + lane < lk ? o : -INFINITY;
   float m = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
   m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
@@ -199,8 +199,8 @@ __device__ __forceinline__ void pool_quad(const Stage1Pool& a, __amdgpu_buffer_r
 // at least 0; the first block's tap 4*first-1 is the last computed column,
 // `carry` (-inf at or past lk).  A block with no tap below lk is -inf.
 __device__ __forceinline__ void pool_tail(const Stage1Pool& a, __amdgpu_buffer_rsrc_t prs,
-                                          int32_t first, int32_t lk, int32_t ob, float carry) {
-  const int lane = threadIdx.x & (kWave - 1);
+                                          int32_t first, int32_t lk, int32_t ob, float carry,
+                                          int lane = threadIdx.x & (kWave - 1)) {
   for (int64_t n = first + lane; n < a.nb; n += kWave) {
     const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
     const bool zero_tap = n == first ? 4 * n < lk : 4 * n - 1 < lk;
@@ -213,8 +213,10 @@ __device__ __forceinline__ void pool_tail(const Stage1Pool& a, __amdgpu_buffer_r
 
 
 // Pooled row of a token outside every sequence: no taps, block of the token 0.
-__device__ __forceinline__ void orphan_pool_row(const Stage1Pool& p, int64_t row) {
-  pool_tail(p, make_rsrc(p.pooled + row * p.nb, static_cast<uint32_t>(p.nb * 4)), 0, 0, 0, -INFINITY);
+__device__ __forceinline__ void orphan_pool_row(const Stage1Pool& p, int64_t row,
+                                                int lane = threadIdx.x & (kWave - 1)) {
+  pool_tail(p, make_rsrc(p.pooled + row * p.nb, static_cast<uint32_t>(p.nb * 4)), 0, 0, 0, -INFINITY,
+            lane);
 }
 
 // ---------------------------------------------------------------- MFMA path
@@ -226,8 +228,8 @@ struct Frag {
   bf16x8 v[kD / 32];
 };
 
-__device__ __forceinline__ Frag load_q_frag(const Stage1Args& a, int64_t t, int g) {
-  const int lane = threadIdx.x & (kWave - 1);
+__device__ __forceinline__ Frag load_q_frag(const Stage1Args& a, int64_t t, int g,
+                                            int lane = threadIdx.x & (kWave - 1)) {
   const __bf16* p = a.q + t * a.q_st + static_cast<int64_t>(g * kG + (lane & 15)) * a.q_sh +
                     8 * (lane >> 4);
   Frag f;
@@ -524,8 +526,8 @@ struct Segment {
 // Rows are r in [0, Hkv*Tq): sequence b owns [Hkv*cu_q[b], Hkv*cu_q[b+1]),
 // group-major inside; rows before Hkv*cu_q[0] / after Hkv*cu_q[B] belong to
 // tokens outside every sequence (all-zero rows).
-__device__ Segment find_segment(const Stage1Args& a, int64_t r, int64_t r_end) {
-  const int lane = threadIdx.x & (kWave - 1);
+__device__ Segment find_segment(const Stage1Args& a, int64_t r, int64_t r_end,
+                                int lane = threadIdx.x & (kWave - 1)) {
   int count = 0;
   for (int64_t base = 0; base <= a.B; base += kWave) {
     const int64_t i = base + lane;
@@ -588,8 +590,8 @@ __device__ __forceinline__ int64_t zigzag(int64_t k, int64_t L) {
 }
 
 template <typename OutT>
-__device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t cols) {
-  const int lane = threadIdx.x & (kWave - 1);
+__device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t cols,
+                                             int lane = threadIdx.x & (kWave - 1)) {
   if constexpr (sizeof(OutT) == 4) {
     if ((cols & 3) == 0 && (from & 3) == 0) {
       for (int64_t j = from + 4 * lane; j < cols; j += 4 * kWave)
@@ -597,7 +599,7 @@ __device__ __forceinline__ void zero_row_vec(OutT* orow, int64_t from, int64_t c
       return;
     }
   }
-  zero_tail<OutT>(orow, from, cols);
+  zero_tail<OutT>(orow, from, cols, lane);
 }
 
 // ------------------------------------------------- pieces of the streaming path
@@ -1281,8 +1283,7 @@ constexpr int kRowWaves = 12;        // 768 threads: three waves per SIMD
 // Keys past the sequence (or past k) read as zero through the buffer range.
 template <int kWaves>
 __device__ __forceinline__ void row_k_issue(const Stage1Args& a, bf16x8* kt, const Segment& sg,
-                                            int ntl, int wave) {
-  const int lane = threadIdx.x & (kWave - 1);
+                                            int ntl, int wave, int lane = threadIdx.x & (kWave - 1)) {
   int64_t keys_ok = readable_keys(a, sg.ks, sg.lk);
   keys_ok = keys_ok < 16 * ntl ? keys_ok : 16 * ntl;
   const __bf16* kb = a.k + (keys_ok > 0 ? static_cast<int64_t>(sg.ks) * a.k_st : 0) +
@@ -1452,9 +1453,17 @@ __device__ __forceinline__ void row_pipeline(KView kl, const Frag& qf, int32_t v
 // leave every lane of group u holding the output of tile u for key l%16,
 // i.e. the quad's 64 outputs in lane order.  The row is written by exactly
 // kOutQ 64-column stores: quads [0, nq) computed, the rest zeros.
-template <typename OutT, int kOutQ, int N>
+// Fused max-pool of one row (kernels instantiated with kPool): the pooled
+// row's descriptor, the sequence's key count and the token's 64-token block.
+struct RowPool {
+  __amdgpu_buffer_rsrc_t prs;
+  int32_t lk;
+  int32_t ob;
+};
+
+template <typename OutT, int kOutQ, int N, bool kPool>
 __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const f16x8 (&pw)[N][2],
-                                          int nq) {
+                                          int nq, const Stage1Pool& pp, const RowPool& rp) {
   const int lane = threadIdx.x & (kWave - 1);
   f16x8 wa, wb;
   {
@@ -1471,6 +1480,7 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
     wb = __builtin_bit_cast(f16x8, u32x4{t == 2 ? w01 : 0u, t == 2 ? w23 : 0u,
                                          t == 3 ? w01 : 0u, t == 3 ? w23 : 0u});
   }
+  [[maybe_unused]] float ov[kOutQ];  // fused pool: the row's outputs, pooled once pw is dead
 #pragma unroll
   for (int qd = 0; qd < kOutQ; ++qd) {
     float o = 0.f;
@@ -1480,7 +1490,22 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb, pw[qd < N ? qd : 0][1], acc, 0, 0, 0);
       o = acc.x;
     }
-    store_out<OutT>(orow + 64 * qd + lane, o);
+    if (!kPool || pp.write_scores) store_out<OutT>(orow + 64 * qd + lane, o);
+    if constexpr (kPool) ov[qd] = o;
+  }
+  if constexpr (kPool) {
+    // The quads past nq hold zero scores: pooled like the stored row.  Blocks
+    // past the row's columns have no tap below lk (lk <= out_cols).  The lane
+    // index is opaque here, so the pool's per-lane offsets are computed here
+    // rather than hoisted out of the row loop (they would stay live across
+    // every row and push its registers into spills).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    float carry = -INFINITY;
+#pragma unroll
+    for (int qd = 0; qd < kOutQ; ++qd)
+      pool_quad(pp, rp.prs, 64 * qd, rp.lk, rp.ob, ov[qd], carry, false, ln);
+    pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
   }
 }
 
@@ -1508,9 +1533,9 @@ __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
 // with peaky keys (x8).  Key 0 alone was no faster on flat scores and 70 %
 // slower on peaky ones, where a fifth of the rows fail the 2^14 check below.
 // Returns false, having stored nothing, when the row needs its exact max.
-template <typename OutT, int NQ, int kOutQ>
+template <typename OutT, int NQ, int kOutQ, bool kPool>
 __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, float c, f16x8 sel,
-                                         OutT* orow) {
+                                         OutT* orow, const Stage1Pool& pp, const RowPool& rp) {
   f16x8 pw[NQ][2];
   f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
   float mc[4];
@@ -1545,7 +1570,7 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
   }
   float L[4];
   if (!row_sums(lsum, L)) return false;
-  row_store<OutT, kOutQ, NQ>(orow, L, pw, NQ);
+  row_store<OutT, kOutQ, NQ, kPool>(orow, L, pw, NQ, pp, rp);
   return true;
 }
 
@@ -1554,12 +1579,15 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
 // stores (computed quads, then zeros).  A row of nq visible quads runs the
 // straight-line row_fast<nq>; a row whose first-tile reference fails runs
 // the general pipeline against its exact max.
-template <typename OutT, int kOutQ>
-__device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Segment& sg,
-                                        int32_t lq, const Frag& qf, f16x8 sel) {
+template <typename OutT, int kOutQ, bool kPool>
+__device__ __forceinline__ void lds_row(const Stage1Args& a, const Stage1Pool& pp, KView kl,
+                                        const Segment& sg, int32_t lq, const Frag& qf, f16x8 sel) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq;
   OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
+  RowPool rp{};
+  if constexpr (kPool)
+    rp = RowPool{make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)), sg.lk, lq >> 6};
   int32_t vis = sg.lk;
   if (a.causal) {
     vis = tdiv16(lq - 15) + sg.lk - tdiv16(sg.lq_len - 16 + 1);
@@ -1571,13 +1599,23 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Seg
   const float c = a.scale_log2;                // > 0 on this path
   if (nq == 0) {
 #pragma unroll
-    for (int qd = 0; qd < kOutQ; ++qd) store_out<OutT>(orow + 64 * qd + lane, 0.f);
+    for (int qd = 0; qd < kOutQ; ++qd)
+      if (!kPool || pp.write_scores) store_out<OutT>(orow + 64 * qd + lane, 0.f);
+    if constexpr (kPool) {
+      int ln = lane;  // opaque: see row_store
+      asm volatile("" : "+v"(ln));
+      float carry = -INFINITY;
+#pragma unroll
+      for (int qd = 0; qd < kOutQ; ++qd)
+        pool_quad(pp, rp.prs, 64 * qd, rp.lk, rp.ob, 0.f, carry, false, ln);
+      pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
+    }
     return;
   }
   bool done = false;
   switch (nq) {
 #define UNUM_ROW_CASE(N) \
-    case N: if constexpr (N <= kOutQ) done = row_fast<OutT, N, kOutQ>(kl, qf, vis, c, sel, orow); break;
+    case N: if constexpr (N <= kOutQ) done = row_fast<OutT, N, kOutQ, kPool>(kl, qf, vis, c, sel, orow, pp, rp); break;
     UNUM_ROW_CASE(1) UNUM_ROW_CASE(2) UNUM_ROW_CASE(3) UNUM_ROW_CASE(4)
     UNUM_ROW_CASE(5) UNUM_ROW_CASE(6) UNUM_ROW_CASE(7) UNUM_ROW_CASE(8)
 #undef UNUM_ROW_CASE
@@ -1606,11 +1644,12 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, KView kl, const Seg
   row_pipeline<kOutQ>(kl, qf, vis, nq, false, c, mc, sel, pw, lsum);
   float L[4];
   row_sums(lsum, L);
-  row_store<OutT, kOutQ, kOutQ>(orow, L, pw, nq);
+  row_store<OutT, kOutQ, kOutQ, kPool>(orow, L, pw, nq, pp, rp);
 }
 
-template <typename OutT, int kOutQ>
-__global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows) {
+template <typename OutT, int kOutQ, bool kPool>
+__global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows,
+                                                                       Stage1Pool pp) {
   __shared__ bf16x8 kt[kLdsUnits];                             // 128 KiB
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & (kWave - 1);
@@ -1627,7 +1666,13 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
   const int64_t r_begin = n_rows * blockIdx.x / gridDim.x;
   const int64_t r_end = n_rows * (blockIdx.x + 1) / gridDim.x;
   for (int64_t r = r_begin; r < r_end;) {
-    const Segment sg = find_segment(a, r, r_end);
+    // The lane index is opaque to the compiler inside each segment, so the
+    // segment-level per-lane addresses (sequence lookup, K block loads,
+    // query loads, orphan rows) are computed here rather than hoisted out of
+    // the loop, where they stayed live across every row and spilled.
+    int sl = lane;
+    asm volatile("" : "+v"(sl));
+    const Segment sg = find_segment(a, r, r_end, sl);
     const int64_t n = sg.end - r;
     __syncthreads();  // the previous segment is done with kt
     // Wave w takes the row pairs (2w, 2w+1), (2w+24, 2w+25), ... of the
@@ -1638,8 +1683,12 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
       for (int64_t j = 0; my_row(j) < n; ++j) {
         const int64_t rel = r + my_row(j) - sg.rlo;
         const int64_t g = rel / sg.nt_orphan, t = sg.t0 + rel % sg.nt_orphan;
-        if (g < a.Hkv && t < a.Tq)
-          zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols);
+        if (g < a.Hkv && t < a.Tq) {
+          if (!kPool || pp.write_scores)
+            zero_row_vec<OutT>(static_cast<OutT*>(a.out) + (g * a.Tq + t) * a.out_cols, 0, a.out_cols,
+                               sl);
+          if constexpr (kPool) orphan_pool_row(pp, g * a.Tq + t, sl);
+        }
       }
       r = sg.end;
       continue;
@@ -1651,14 +1700,14 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
     if (sg.lk > 0) {
       int ntl = 4 * ((sg.lk + 63) >> 6);
       ntl = ntl < 4 * kOutQ ? ntl : 4 * kOutQ;
-      row_k_issue<kRowWaves>(a, kt, sg, ntl, wave);
+      row_k_issue<kRowWaves>(a, kt, sg, ntl, wave, sl);
     }
     const bool any = my_row(0) < n;
     int32_t lq_n = 0;
     Frag qn;
     if (any) {
       lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(0), sg.lq_len));
-      qn = load_q_frag(a, sg.qs + lq_n, sg.g);
+      qn = load_q_frag(a, sg.qs + lq_n, sg.g, sl);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // kt is filled
@@ -1672,9 +1721,9 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
       // The next row's queries load into registers while this row computes.
       if (my_row(j + 1) < n) {
         lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(j + 1), sg.lq_len));
-        qn = load_q_frag(a, sg.qs + lq_n, sg.g);
+        qn = load_q_frag(a, sg.qs + lq_n, sg.g, sl);
       }
-      lds_row<OutT, kOutQ>(a, kl, sg, lq, qf, sel);
+      lds_row<OutT, kOutQ, kPool>(a, pp, kl, sg, lq, qf, sel);
     }
     r = sg.end;
   }
@@ -1978,23 +2027,42 @@ int launch_split(const Stage1Args& a, const Stage1Pool& pp, const SplitPlan& pla
   return check_launch(op);
 }
 
+// The LDS-resident kernel: one persistent workgroup per CU, instantiated per
+// output quads (out_cols / 64 of 1..8).
+template <typename OutT, bool kPool>
+void launch_lds(const Stage1Args& a, const Stage1Pool& pp, int64_t n_rows, hipStream_t s) {
+  int64_t grid = (n_rows + kRowWaves - 1) / kRowWaves;
+  const int64_t cus = num_cus();
+  grid = grid < cus ? grid : cus;
+  const dim3 g(static_cast<unsigned>(grid)), b(kRowWaves * kWave);
+  switch (a.out_cols / 64) {
+#define UNUM_LDS_CASE(N) \
+    case N: hipLaunchKernelGGL((stage1_lds_kernel<OutT, N, kPool>), g, b, 0, s, a, n_rows, pp); break;
+    UNUM_LDS_CASE(1) UNUM_LDS_CASE(2) UNUM_LDS_CASE(3) UNUM_LDS_CASE(4)
+    UNUM_LDS_CASE(5) UNUM_LDS_CASE(6) UNUM_LDS_CASE(7)
+#undef UNUM_LDS_CASE
+    default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8, kPool>), g, b, 0, s, a, n_rows, pp); break;
+  }
+}
+
 template <typename OutT, bool kPool>
 int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t ws_bytes,
                   hipStream_t s) {
   const Stage1Path path = stage1_path<OutT>(a);
-  // The pool is fused into the K-streaming kernel only: in the LDS-resident
-  // kernel (rows of at most 512 keys) the extra state pushed the row's
-  // registers into spills, and the two separate kernels measured faster.
-  if (kPool && path != kPathStream)
+  // The pool is fused into the K-streaming and LDS-resident kernels (the MFMA
+  // paths); other shapes run the two ops.
+  if (kPool && path != kPathStream && path != kPathLds)
     UNUM_FAIL(UNUM_ERR_UNSUPPORTED,
-              "infllmv2_attn_stage1_maxpool: fused only for rows over 512 keys with G=16, "
-              "D=128, 16-byte aligned q/k and a positive scale (got G=%d, D=%d, %lld columns)",
+              "infllmv2_attn_stage1_maxpool: fused only on the MFMA paths: G=16, D=128, "
+              "16-byte aligned q/k and a positive scale (got G=%d, D=%d, %lld columns)",
               a.G, a.D, (long long)a.out_cols);
   const int64_t n_rows = static_cast<int64_t>(a.Hkv) * a.Tq;
   if (path == kPathStream && piece_grid(a.Hkv, a.Tq, a.B, kStSplitWaves * kStTokensPerWave) > INT32_MAX)
     UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT, "infllmv2_attn_stage1: %lld tokens and %lld sequences are too many",
               (long long)a.Tq, (long long)a.B);
-  if constexpr (kPool) {
+  if (kPool && path == kPathLds) {
+    launch_lds<OutT, kPool>(a, pp, n_rows, s);
+  } else if constexpr (kPool) {
     // Key splits when the caller gave the workspace they need, else whole rows.
     const SplitPlan plan = split_plan(a.Hkv, a.Tq, a.B, a.out_cols);
     if (plan.n_splits >= 2 && ws != nullptr && ws_bytes >= plan.bytes)
@@ -2005,18 +2073,7 @@ int launch_stage1(const Stage1Args& a, const Stage1Pool& pp, void* ws, int64_t w
                        dim3(static_cast<unsigned>(grid)), dim3(kStWaves * kWave), 0, s, a, pp,
                        Stage1Split{});
   } else if (path == kPathLds) {
-    int64_t grid = (n_rows + kRowWaves - 1) / kRowWaves;
-    const int64_t cus = num_cus();
-    grid = grid < cus ? grid : cus;
-    const dim3 g(static_cast<unsigned>(grid)), b(kRowWaves * kWave);
-    switch (a.out_cols / 64) {
-#define UNUM_LDS_CASE(N) \
-      case N: hipLaunchKernelGGL((stage1_lds_kernel<OutT, N>), g, b, 0, s, a, n_rows); break;
-      UNUM_LDS_CASE(1) UNUM_LDS_CASE(2) UNUM_LDS_CASE(3) UNUM_LDS_CASE(4)
-      UNUM_LDS_CASE(5) UNUM_LDS_CASE(6) UNUM_LDS_CASE(7)
-#undef UNUM_LDS_CASE
-      default: hipLaunchKernelGGL((stage1_lds_kernel<OutT, 8>), g, b, 0, s, a, n_rows); break;
-    }
+    launch_lds<OutT, false>(a, pp, n_rows, s);
   } else if (path == kPathStream && decode_batch(a)) {
     // Decode batches (at most two new tokens per sequence on average): one
     // workgroup per row, the waves splitting its keys.

@@ -166,9 +166,11 @@ def infllmv2_attn_stage1_maxpool(q, k, cu_seqlens_q, cu_seqlens_k, max_context_l
     cu_seqlens_k, zeros, max_seqlen_q=16 * Kp, max_context_len, local_blocks,
     init_blocks)`` -- each row pooled in place, as the selection pipeline
     chains the two ops -- computed in one kernel, so the fp32 scores only go
-    to HBM when ``return_scores`` asks for them (then ``(pooled, scores)``).
-    Shapes off the MFMA paths (G != 16, D != 128, ...) and ``block_size /
-    stride`` other than 64 / 16 run the two ops separately.
+    to HBM when ``return_scores`` asks for them (then ``(pooled, scores)``):
+    rows of at most 512 keys pool in the LDS-resident stage-1 kernel, longer
+    rows in the key-streaming kernels.  Shapes off the MFMA paths (G != 16,
+    D != 128, ...) and ``block_size / stride`` other than 64 / 16 run the two
+    ops separately.
     """
     op = "infllmv2_attn_stage1_maxpool"
     dev = require_gpu(op, q, k, cu_seqlens_q, cu_seqlens_k)
