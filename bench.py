@@ -476,12 +476,21 @@ def main():
     for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5"),
                       ("stage1_maxpool_cfg4", "stage1_cfg4")):
         if name in per_op and src in comps:
+            # the unfused kernel's bytes with its score tensor replaced by the
+            # pooled tensor (both sizes read off one call's outputs)
+            fns = dict(ops + extra)
+            scores, pooled = fns[src](), fns[name]()
             flop = comps[src]["flop"]
+            nbytes = comps[src]["bytes"] - scores.numel() * scores.element_size() \
+                + pooled.numel() * pooled.element_size()
             t = per_op[name] * 1e-3
             comps[name] = dict(us=per_op[name] * 1e3, tflops=flop / t / 1e12,
                                pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                               gbs=nbytes / t / 1e9,
+                               pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                               flop=flop, bytes=nbytes, bound=comps[src]["bound"],
                                config=f"{src} fused with the max-pool: pooled fp32 "
-                                      "[Hkv, Tq, NB] only (scores not stored)")
+                                      f"{list(pooled.shape)} only (scores not stored)")
     if "compress_keys_cfg5" in per_op:
         nbytes = 2 * 135168 * 2 * 128 + 2 * 8447 * 2 * 128
         t = per_op["compress_keys_cfg5"] * 1e-3
