@@ -1513,13 +1513,11 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
 // exceeds 2^14 (the first-tile reference was too low for f16).
 __device__ __forceinline__ bool row_sums(const f32x4& lsum, float (&L)[4]) {
   const float lv[4] = {lsum.x, lsum.y, lsum.z, lsum.w};
-  bool bad = false;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    L[r] = grp_sum16(lv[r]);
-    bad = bad || !(L[r] <= static_cast<float>(kRowSumLimit));
-  }
-  return __builtin_amdgcn_ballot_w64(bad) == 0;
+  for (int r = 0; r < 4; ++r) L[r] = grp_sum16(lv[r]);
+  // One compare of the largest sum (an overflow to inf fails it too).
+  const float m = fmaxf(fmaxf(L[0], L[1]), fmaxf(L[2], L[3]));
+  return __builtin_amdgcn_ballot_w64(!(m <= static_cast<float>(kRowSumLimit))) == 0;
 }
 
 // A row of exactly NQ visible quads, as one straight-line block: the scores,
