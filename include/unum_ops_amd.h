@@ -307,7 +307,9 @@ int unum_sparse_paged_attention(const void* q, int64_t q_stride_t, int64_t q_str
  *          h_m = sum over the stride tokens stride*m .. stride*m+stride-1 of
  *          the sequence, in fp32 in token order.
  * kernel_size == 2 * stride == 32; D % 8 == 0 and H*D/8 <= 64;
- * windows_per_unit a multiple of 64 / (H*D/8).
+ * windows_per_unit a multiple of the lane groups per wave, 64 / (H*D/w) with
+ * w = 4 when H*D/4 <= 64 and w = 8 otherwise (a multiple of 64 / (H*D/8)
+ * always is one).
  */
 int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_stride_h,
                        const int32_t* cu_seqlens_raw, const int32_t* cu_seqlens_comp,

@@ -44,9 +44,11 @@ class CompressionPlan:
         self.kernel_size, self.stride, self.H, self.D = kernel_size, stride, H, D
         # Windows per lane group: a group loads and sums each half-block of
         # its run of windows once, so longer runs load less; about 512 waves
-        # in all measured fastest (8 windows a group on cfg5's 8447 windows,
-        # 16 on 18.7K), at most 16 a group.
-        groups = 64 // max(1, H * (D // 8))
+        # in all measured fastest, at most 16 windows a group.  A lane takes
+        # 4 elements of a token row when the row fits a wave that way, else
+        # 8 (the kernel's rule), which sets the groups per wave.
+        slice_elems = 4 if H * (D // 4) <= 64 else 8
+        groups = 64 // max(1, H * (D // slice_elems))
         per_group = max(1, min(16, self.total // (512 * max(groups, 1))))
         self.per_unit = per_group * max(groups, 1)
         units = (lk + self.per_unit - 1) // self.per_unit

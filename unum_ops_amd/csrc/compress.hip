@@ -13,9 +13,9 @@
 // (kernel a power of two: the scale is exact).
 //
 // Work decomposition: a wave owns a unit of consecutive windows of one
-// sequence; each lane owns one 8-element slice (16 bytes) of one head, a row
-// of the group's lanes covering all heads and dims of a token, and the
-// wave's lane groups split the unit's windows between them.  A lane group
+// sequence; each lane owns one 4- or 8-element slice (8 or 16 bytes) of one
+// head, a row of the group's lanes covering all heads and dims of a token,
+// and the wave's lane groups split the unit's windows between them.  A lane group
 // walks its consecutive windows loading and summing every half-block once
 // (16 token loads at once, the next half-block's while the current one is
 // summed): each raw key is read once.
@@ -47,57 +47,82 @@ __device__ __forceinline__ int find_seq(const int32_t* prefix, int64_t B, int64_
   return count - 1;
 }
 
-__device__ __forceinline__ void add8(float* acc, i32x4 w) {
-  const uint32_t u[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// A lane's slice of kSW bf16 elements of one token row (16 or 8 bytes).
+template <int kSW>
+struct SliceT;
+template <>
+struct SliceT<8> {
+  typedef i32x4 type;
+};
+template <>
+struct SliceT<4> {
+  typedef i32x2 type;
+};
+
+template <int kSW>
+__device__ __forceinline__ void add_slice(float* acc, typename SliceT<kSW>::type w) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    acc[2 * e] += __uint_as_float(u[e] << 16);
-    acc[2 * e + 1] += __uint_as_float(u[e] & 0xffff0000u);
+  for (int e = 0; e < kSW / 2; ++e) {
+    const uint32_t u = static_cast<uint32_t>(w[e]);
+    acc[2 * e] += __uint_as_float(u << 16);
+    acc[2 * e + 1] += __uint_as_float(u & 0xffff0000u);
   }
 }
 
 // Half-block hb of a lane's slice: its kStride token rows, loaded at once.
-template <int kStride>
-__device__ __forceinline__ void half_load(const __bf16* kb, int64_t k_st, int64_t hb, i32x4 (&w)[kStride]) {
+template <int kStride, int kSW>
+__device__ __forceinline__ void half_load(const __bf16* kb, int64_t k_st, int64_t hb,
+                                          typename SliceT<kSW>::type (&w)[kStride]) {
 #pragma unroll
-  for (int i = 0; i < kStride; ++i) w[i] = *reinterpret_cast<const i32x4*>(kb + (hb * kStride + i) * k_st);
+  for (int i = 0; i < kStride; ++i)
+    w[i] = *reinterpret_cast<const typename SliceT<kSW>::type*>(kb + (hb * kStride + i) * k_st);
 }
 
 // Their sum, in token order.
-template <int kStride>
-__device__ __forceinline__ void half_sum(const i32x4 (&w)[kStride], float* h) {
+template <int kStride, int kSW>
+__device__ __forceinline__ void half_sum(const typename SliceT<kSW>::type (&w)[kStride], float* h) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = 0.f;
+  for (int e = 0; e < kSW; ++e) h[e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < kStride; ++i) add8(h, w[i]);
+  for (int i = 0; i < kStride; ++i) add_slice<kSW>(h, w[i]);
 }
 
 // Window j = (half-block j + half-block j+1) / kernel, rounded to bf16.
+template <int kSW>
 __device__ __forceinline__ void store_window(uint16_t* o, const float* h0, const float* h1, float inv) {
-  uint32_t pk[4];
+  typename SliceT<kSW>::type v;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < kSW / 2; ++e) {
     const uint32_t lo = f32_to_bf16_bits((h0[2 * e] + h1[2 * e]) * inv);
     const uint32_t hi = f32_to_bf16_bits((h0[2 * e + 1] + h1[2 * e + 1]) * inv);
-    pk[e] = lo | (hi << 16);
+    v[e] = static_cast<int>(lo | (hi << 16));
   }
-  *reinterpret_cast<i32x4*>(o) = i32x4{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+  *reinterpret_cast<typename SliceT<kSW>::type*>(o) = v;
 }
 
-template <int kStride>
+// Lanes per token row take kSW-element slices: 8 bytes when a row fits in
+// the wave that way (twice the waves for the same windows per lane, so twice
+// the loads in flight: cfg5's keys measured faster), 16 bytes otherwise.
+__host__ __device__ inline int slice_elems(int64_t H, int64_t D) {
+  return H * (D / 4) <= kWave ? 4 : 8;
+}
+
+template <int kStride, int kSW>
 __global__ __launch_bounds__(256) void compress_keys_kernel(CompressArgs a) {
   const int64_t unit = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
   if (unit >= a.n_units) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
   const int b = find_seq(a.unit_prefix, a.B, unit);
   if (b < 0 || b >= a.B) return;
-  const int32_t slices = a.D / 8;               // 16-byte slices per head
+  const int32_t slices = a.D / kSW;             // slices per head
   const int32_t row_lanes = a.H * slices;       // lanes per token row
   const int32_t groups = kWave / row_lanes;
   const int32_t grp = lane / row_lanes;
   if (grp >= groups) return;                    // lanes past the last full group
   const int32_t h = (lane % row_lanes) / slices;
-  const int32_t d0 = 8 * ((lane % row_lanes) % slices);
+  const int32_t d0 = kSW * ((lane % row_lanes) % slices);
   const int64_t run = unit - a.unit_prefix[b];
   // Windows of the sequence, clamped to what its raw keys (inside the key
   // tensor) and its output rows (inside the output) allow.
@@ -118,21 +143,21 @@ __global__ __launch_bounds__(256) void compress_keys_kernel(CompressArgs a) {
   // Windows j_lo .. j_hi-1 use half-blocks j_lo .. j_hi, each loaded and
   // summed once; two register buffers alternate, so the next half-block
   // loads while the current one is summed.
-  i32x4 w0[kStride], w1[kStride];
-  float hp[8], hn[8];
-  half_load<kStride>(kb, a.k_st, j_lo, w0);
-  half_load<kStride>(kb, a.k_st, j_lo + 1, w1);
-  half_sum<kStride>(w0, hp);
+  typename SliceT<kSW>::type w0[kStride], w1[kStride];
+  float hp[kSW], hn[kSW];
+  half_load<kStride, kSW>(kb, a.k_st, j_lo, w0);
+  half_load<kStride, kSW>(kb, a.k_st, j_lo + 1, w1);
+  half_sum<kStride, kSW>(w0, hp);
   for (int64_t j = j_lo; j < j_hi; j += 2) {
     // w1 holds half-block j+1
-    if (j + 2 <= j_hi) half_load<kStride>(kb, a.k_st, j + 2, w0);
-    half_sum<kStride>(w1, hn);
-    store_window(ob + j * o_st, hp, hn, a.inv_kernel);
+    if (j + 2 <= j_hi) half_load<kStride, kSW>(kb, a.k_st, j + 2, w0);
+    half_sum<kStride, kSW>(w1, hn);
+    store_window<kSW>(ob + j * o_st, hp, hn, a.inv_kernel);
     if (j + 1 >= j_hi) break;
     // w0 holds half-block j+2
-    if (j + 3 <= j_hi) half_load<kStride>(kb, a.k_st, j + 3, w1);
-    half_sum<kStride>(w0, hp);
-    store_window(ob + (j + 1) * o_st, hn, hp, a.inv_kernel);
+    if (j + 3 <= j_hi) half_load<kStride, kSW>(kb, a.k_st, j + 3, w1);
+    half_sum<kStride, kSW>(w0, hp);
+    store_window<kSW>(ob + (j + 1) * o_st, hn, hp, a.inv_kernel);
   }
 }
 
@@ -162,7 +187,7 @@ extern "C" int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_s
   UNUM_REQUIRE((reinterpret_cast<uintptr_t>(k) & 15) == 0 && (k_stride_t % 8) == 0 &&
                    (k_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
                "compress_keys: keys and output must be 16-byte aligned (strides %% 8 == 0)");
-  const int32_t groups = static_cast<int32_t>(kWave / (H * (D / 8)));
+  const int32_t groups = static_cast<int32_t>(kWave / (H * (D / slice_elems(H, D))));
   UNUM_REQUIRE(windows_per_unit % groups == 0,
                "compress_keys: windows_per_unit=%d not a multiple of the %d lane groups",
                windows_per_unit, groups);
@@ -185,7 +210,11 @@ extern "C" int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_s
   a.stride = stride;
   a.per_group = windows_per_unit / groups;
   a.inv_kernel = 1.0f / static_cast<float>(kernel_size);
-  hipLaunchKernelGGL(compress_keys_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (slice_elems(H, D) == 4)
+    hipLaunchKernelGGL((compress_keys_kernel<16, 4>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL((compress_keys_kernel<16, 8>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
   return check_launch("compress_keys");
 }
