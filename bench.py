@@ -46,7 +46,7 @@ def parse():
                                        "stage1_peaky", "stage1_cfg5_h16", "maxpool_cfg5_h16",
                                        "block_table_cfg5_h16", "block_table_cfg4",
                                        "stage1_maxpool_cfg4", "stage2_cfg5", "stage2_cfg4",
-                                       "copy"],
+                                       "topk_cfg5", "select_cfg5", "copy"],
                     default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
@@ -92,7 +92,7 @@ def build_inputs(dev):
               max_context_len=p5["max_context_len"], scores=sc,
               cache=torch.zeros(1, dtype=torch.int32, device=dev),
               cu_q_cpu=p5["cu_seqlens_q"], cu_k_cpu=p5["cu_seqlens_k"])
-    del pooled
+    c5["pooled"] = pooled
     # cfg4: 64 decode / chunked-prefill sequences (1-16 new tokens after
     # 16K-64K cached ones), stage 1 over their compressed keys.
     p4 = workloads.cfg4_pipeline()
@@ -160,7 +160,7 @@ def main():
     from unum_ops_amd.compression import CompressionPlan, compress_keys
     from unum_ops_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_maxpool,
                                         max_pooling_1d_varlen)
-    from unum_ops_amd.pipeline import maxpool_topk
+    from unum_ops_amd.pipeline import maxpool_topk, select_blocks, topk_blocks
     from unum_ops_amd.sparse_attention import sparse_paged_attention
     from unum_ops_amd.sparse_kernel_extension import get_block_table
 
@@ -275,6 +275,14 @@ def main():
                                       b["topk_idx"], b["block_table"], b["token_to_bs"],
                                       b["token_pos_in_bs"], b["seqlen_q"])
 
+    def op_topk_pooled_cfg5():
+        return topk_blocks(c5["pooled"], 64)
+
+    def op_select_cfg5():
+        return select_blocks(c5["q"], c5["k"], c5["cu_q"], c5["cu_k"], bt["block_table"],
+                             bt["token_to_bs"], bt["token_pos_in_bs"], bt["seqlen_q"],
+                             c5["max_context_len"], max_seqlen_k=c5["max_seqlen_k"], topk=64)
+
     def op_stage1_maxpool_cfg4():
         return infllmv2_attn_stage1_maxpool(c4["q"], c4["k"], c4["cu_q"], c4["cu_k"],
                                             c4["max_context_len"],
@@ -293,7 +301,8 @@ def main():
              ("block_table_cfg5_h16", op_block_table_cfg5_h16),
              ("block_table_cfg4", op_block_table_cfg4),
              ("stage1_maxpool_cfg4", op_stage1_maxpool_cfg4),
-             ("stage2_cfg5", op_stage2_cfg5), ("stage2_cfg4", op_stage2_cfg4)]
+             ("stage2_cfg5", op_stage2_cfg5), ("stage2_cfg4", op_stage2_cfg4),
+             ("topk_cfg5", op_topk_pooled_cfg5), ("select_cfg5", op_select_cfg5)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -421,6 +430,20 @@ def main():
                                pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
                                config=("cfg2 input" if name == "maxpool_topk" else "cfg5 scores")
                                + " -> top-64 block ids int32 [2, T, 64]")
+
+    if "topk_cfg5" in per_op:
+        rows, nbk = 2 * int(c5["cu_q_cpu"][-1]), -(-c5["max_context_len"] // 64)
+        nbytes = 4 * rows * nbk + 4 * rows * 64           # pooled rows read, ids written
+        t = per_op["topk_cfg5"] * 1e-3
+        comps["topk_cfg5"] = dict(us=per_op["topk_cfg5"] * 1e3, gbs=nbytes / t / 1e9,
+                                  pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
+                                  config="cfg5 pooled fp32 [2,4096,2112] -> top-64 block ids "
+                                         "int32 [2,4096,64]")
+    if "select_cfg5" in per_op:
+        comps["select_cfg5"] = dict(
+            us=per_op["select_cfg5"] * 1e3,
+            config="select_blocks on cfg5 end to end: stage 1 with the max-pool in its kernel, "
+                   "top-64 over the pooled rows, block table int32 [4096,2,4096]")
 
     if "stage1_cfg5_h16" in per_op:
         flop, nbytes, _ = workloads.stage1_work(c5["cu_q_cpu"], c5["cu_k_cpu"], 16, 1, 128,

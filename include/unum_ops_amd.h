@@ -218,6 +218,23 @@ int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_numel,
                                     void* stream);
 
 /*
+ * The block selection of unum_max_pooling_1d_varlen_topk over rows already
+ * pooled (e.g. the output of unum_infllmv2_attn_stage1_maxpool).  No single
+ * reference function: the top-k the reference's tests apply to pooled scores
+ * (test/test_sparse_kernel.py:42-43), with the same deterministic tie-break.
+ *
+ *   pooled   fp32, `rows` rows of num_blocks scores, row r at r * row_stride
+ *   topk_idx int32 [rows, topk] contiguous, as unum_max_pooling_1d_varlen_topk
+ *            writes it: the topk largest scores, equal scores in ascending
+ *            block id, listed in ascending id; -1 for a selected block
+ *            scoring -inf and for every slot past num_blocks, -1 entries first.
+ * 1 <= num_blocks <= 4096 (when rows > 0), row_stride >= num_blocks,
+ * rows < 2^33; NaN scores are outside the contract.
+ */
+int unum_topk_blocks(const float* pooled, int64_t rows, int64_t row_stride, int64_t num_blocks,
+                     int32_t* topk_idx, int32_t topk, void* stream);
+
+/*
  * Top-k block ids -> per-token paged KV slots, replacing
  * get_block_table_ref_torch (get_table_torch.py:4-44) and the exported
  * get_block_table_v2/_v3 (get_table_triton.py:218-264, kernel :6-67).

@@ -3,8 +3,8 @@ block table) on the chunked-prefill/decode mix and the long-context chunk.
 
 Each stage is checked against the oracle on the same input the GPU stage saw:
 stage-1 scores within atol 1e-3 / rtol 1e-2 of the fp32 oracle, the max-pool
-of the GPU scores bit-exact, the top-k ids equal to a CPU top-k of the GPU
-pooled scores, and the block table of those ids bit-exact.  The block ids the
+of the GPU scores bit-exact, the top-k ids equal to the oracle's top-k of the
+GPU pooled scores, and the block table of those ids bit-exact.  The block ids the
 oracle end to end selects may differ from the GPU's only where two pooled
 scores are within rounding of each other, so their agreement is a recall
 figure, not an equality.
@@ -16,7 +16,7 @@ import torch
 
 import oracle
 import workloads
-from unum_ops_amd.pipeline import select_blocks, topk_blocks
+from unum_ops_amd.pipeline import select_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +49,7 @@ def _check_pipeline(p, dev, min_recall):
                                          16 * kp, p["max_context_len"], 1, 1)
     np.testing.assert_array_equal(pooled_c.numpy(), exp_p)
 
-    np.testing.assert_array_equal(idx_c.numpy(), topk_blocks(pooled_c, TOPK).numpy())
+    np.testing.assert_array_equal(idx_c.numpy(), oracle.topk_blocks(pooled_c, TOPK))
 
     # select_blocks multiplies by H, as the reference's exported Triton
     # functions do (get_table_triton.py:259).
@@ -58,10 +58,18 @@ def _check_pipeline(p, dev, min_recall):
                                    head_group=idx_c.shape[0])
     np.testing.assert_array_equal(table.cpu().numpy(), exp_t)
 
+    # Without intermediates, stage 1 pools in its kernel and the top-k runs
+    # over the pooled rows: the same table, bit for bit.
+    fast = select_blocks(
+        g["q"], g["k"], g["cu_seqlens_q"], g["cu_seqlens_k"], g["block_table"],
+        g["token_to_bs"], g["token_pos_in_bs"], g["seqlen_q"], p["max_context_len"],
+        max_seqlen_k=p["max_seqlen_k"], topk=TOPK)
+    assert torch.equal(fast, table)
+
     # Selection agreement with the all-oracle pipeline.
     ref_pool = torch.from_numpy(oracle.max_pooling_1d_varlen(
         exp_s, p["cu_seqlens_q"], p["cu_seqlens_k"], cache, 16 * kp, p["max_context_len"], 1, 1))
-    ref_idx = topk_blocks(ref_pool, TOPK).numpy()
+    ref_idx = oracle.topk_blocks(ref_pool, TOPK)
     got = idx_c.numpy()
     hits = total = 0
     for h in range(got.shape[0]):

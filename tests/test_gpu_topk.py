@@ -14,7 +14,7 @@ import torch
 from oracle.maxpool import max_pooling_1d_varlen as oracle_pool
 from oracle.topk import topk_blocks as oracle_topk
 import workloads
-from unum_ops_amd.pipeline import maxpool_topk
+from unum_ops_amd.pipeline import maxpool_topk, topk_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -129,3 +129,72 @@ def test_unfused_shapes(dev):
     _check(d, dev, 32, **_kw(16 * 1100, 64 * 4100))     # 4100 blocks > 4096
     db = dict(d, input=d["input"].to(torch.bfloat16))
     _check(db, dev, 32, **_kw(16 * 1100, 64 * 300))     # bf16 input
+
+
+# ----------------------------------------------------------------------------
+# topk_blocks: the same selection over rows already pooled (one kernel, the
+# selection of the fused kernel above) -- bit-exact against the oracle.
+
+def _pooled_rows(H, T, NB, seed, ties=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(H, T, NB, generator=g)
+    if ties:
+        x = torch.floor(x * 3.0) / 3.0
+    r = torch.rand(H, T, NB, generator=g)
+    x = torch.where(r < 0.05, torch.full_like(x, float("-inf")), x)
+    x = torch.where(r > 0.98, torch.full_like(x, float("inf")), x)
+    return x
+
+
+@pytest.mark.parametrize("NB", [1, 3, 63, 64, 128, 255, 256, 257, 1000, 2112, 4096])
+@pytest.mark.parametrize("topk", [1, 64, 100])
+def test_topk_blocks_matches_oracle(NB, topk, dev):
+    x = _pooled_rows(2, 37, NB, seed=NB * 7 + topk, ties=NB % 2 == 1)
+    got = topk_blocks(x.to(dev), topk)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
+
+
+def test_topk_blocks_small_cases(dev):
+    inf = float("inf")
+    pooled = torch.tensor([[[0.5, -inf, 2.0, inf, 0.1, -inf],
+                            [-inf, -inf, -inf, -inf, 3.0, -inf]]])
+    assert topk_blocks(pooled.to(dev), 4).cpu().tolist() == [[[0, 2, 3, 4], [-1, -1, -1, 4]]]
+    assert topk_blocks(torch.tensor([[[1.0, 3.0, 2.0]]]).to(dev), 5).cpu().tolist() == \
+        [[[-1, -1, 0, 1, 2]]]
+    ties = torch.tensor([[[1.0, 2.0, 2.0, 2.0, 0.5, 2.0]]]).to(dev)
+    assert topk_blocks(ties, 2).cpu().tolist() == [[[1, 2]]]
+    assert topk_blocks(ties, 4).cpu().tolist() == [[[1, 2, 3, 5]]]
+
+
+def test_topk_blocks_bf16_strided_and_wide(dev):
+    x = _pooled_rows(3, 20, 300, seed=11, ties=True)
+    wide = torch.zeros(3, 20, 320)
+    wide[..., 7:307] = x
+    got = topk_blocks(wide.to(dev)[..., 7:307], 64)            # non-contiguous rows
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, 64))
+    xb = x.to(torch.bfloat16)
+    got = topk_blocks(xb.to(dev), 64)                           # converted to fp32 exactly
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(xb.float(), 64))
+    # past 4096 blocks a row: the device sort, same order
+    x = _pooled_rows(1, 5, 5000, seed=12, ties=True)
+    got = topk_blocks(x.to(dev), 64)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, 64))
+
+
+def test_topk_blocks_of_fused_stage1_maxpool(dev):
+    # The fused stage-1 + max-pool output of cfg5's chunk, then the top-k: the
+    # same ids as the fused pool + top-k over stage 1's scores.
+    from unum_ops_amd.infllm_v2 import infllmv2_attn_stage1_maxpool
+    p = workloads.cfg5_pipeline()
+    g = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+    pooled, scores = infllmv2_attn_stage1_maxpool(
+        g["q"], g["k"], g["cu_seqlens_q"], g["cu_seqlens_k"], p["max_context_len"],
+        max_seqlen_k=p["max_seqlen_k"], return_scores=True)
+    got = topk_blocks(pooled, 64)
+    kp = scores.shape[-1]
+    exp = maxpool_topk(scores, g["cu_seqlens_q"], g["cu_seqlens_k"],
+                       torch.zeros(1, dtype=torch.int32, device=dev), max_seqlen_q=16 * kp,
+                       max_context_len=p["max_context_len"], local_blocks=1, init_blocks=1, topk=64)
+    assert torch.equal(got, exp)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(pooled.cpu(), 64))

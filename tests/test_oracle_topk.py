@@ -5,7 +5,6 @@ import pytest
 import torch
 
 from oracle.topk import topk_blocks, topk_blocks_bruteforce
-from unum_ops_amd.pipeline import topk_blocks as topk_blocks_torch
 
 INF = float("inf")
 
@@ -37,9 +36,22 @@ def test_against_torch_topk_on_distinct_scores(seed):
         np.testing.assert_array_equal(topk_blocks(x, k), ref)
 
 
-def test_matches_the_pipeline_glue():
+def _topk_torch_sort(x, k):
+    """The same rule through torch's stable descending sort (another library's
+    sort than the oracle's numpy argsort)."""
+    H, T, NB = x.shape
+    kk = min(k, NB)
+    vals, idx = torch.sort(x, dim=-1, descending=True, stable=True)
+    vals, idx = vals[..., :kk], idx[..., :kk]
+    idx = torch.where(vals == -INF, torch.full_like(idx, -1), idx).sort(dim=-1).values
+    if kk < k:
+        idx = torch.cat([torch.full((H, T, k - kk), -1, dtype=idx.dtype), idx], dim=-1)
+    return idx.to(torch.int32)
+
+
+def test_matches_a_torch_stable_sort():
     g = torch.Generator().manual_seed(9)
     x = torch.randint(-3, 4, (2, 11, 100), generator=g).float()
     x[x == -3] = -INF
     for k in (5, 64, 120):
-        np.testing.assert_array_equal(topk_blocks(x, k), topk_blocks_torch(x, k).numpy())
+        np.testing.assert_array_equal(topk_blocks(x, k), _topk_torch_sort(x, k).numpy())

@@ -88,6 +88,11 @@ SIGNATURES = {
         _i32,                      # topk
         _p,                        # stream
     ]),
+    "unum_topk_blocks": (ctypes.c_int, [
+        _p, _i64, _i64, _i64,      # pooled, rows, row_stride, num_blocks
+        _p, _i32,                  # topk_idx, topk
+        _p,                        # stream
+    ]),
     "unum_compress_keys": (ctypes.c_int, [
         _p, _i64, _i64,            # k, k_stride_t, k_stride_h
         _p, _p, _p, _i64,          # cu_seqlens_raw, cu_seqlens_comp, unit_prefix, n_units

@@ -501,6 +501,37 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   topk_select<NCH>(key, NB, K, topk + row * K, short_list[threadIdx.x >> 6]);
 }
 
+// The same selection over rows already pooled (the fused stage-1 + max-pool
+// output): one wave per row of `pooled` ([rows, row_stride] fp32, NB blocks
+// a row), lane l holding blocks 256*ch + 4l .. +3 as in the fused kernel, so
+// the ids are the ones maxpool_topk_kernel writes for the same pooled row.
+template <int NCH, bool kVec>
+__global__ __launch_bounds__(256) void topk_rows_kernel(const float* pooled, int64_t rows,
+                                                        int64_t row_stride, int32_t NB,
+                                                        int32_t* topk, int32_t K) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  if (row >= rows) return;  // wave-uniform
+  const int lane = threadIdx.x & (kWave - 1);
+  const float* src = pooled + row * row_stride;
+  __shared__ uint32_t short_list[4][kTopkShortList];
+  uint32_t key[NCH][4];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    const int32_t n0 = 256 * ch + 4 * lane;
+    float r[4];
+    if (kVec && n0 + 3 < NB) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + n0);
+      r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = n0 + e < NB ? src[n0 + e] : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[ch][e] = n0 + e < NB ? order_key(r[e]) : 0u;
+  }
+  topk_select<NCH>(key, NB, K, topk + row * K, short_list[threadIdx.x >> 6]);
+}
+
 // General path: any P >= 1 (window of P+1 taps, padding 1); one output per lane.
 template <typename T>
 __global__ __launch_bounds__(256) void maxpool_generic_kernel(PoolArgs a) {
@@ -688,4 +719,45 @@ extern "C" int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_
   a.init_blocks = init_blocks;
   a.n_chunks = (num_blocks + 255) / 256;
   return launch_topk(a, topk_idx, topk, pooled != nullptr ? 1 : 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int unum_topk_blocks(const float* pooled, int64_t rows, int64_t row_stride,
+                                int64_t num_blocks, int32_t* topk_idx, int32_t topk,
+                                void* stream) {
+  using namespace unum;
+  clear_error();
+  UNUM_REQUIRE(rows >= 0 && num_blocks >= 0 && row_stride >= num_blocks,
+               "topk_blocks: bad sizes (rows=%lld, row_stride=%lld, num_blocks=%lld)",
+               (long long)rows, (long long)row_stride, (long long)num_blocks);
+  UNUM_REQUIRE(topk >= 1, "topk_blocks: topk=%d", topk);
+  UNUM_REQUIRE(num_blocks <= kTopkMaxChunks * 256, "topk_blocks: %lld blocks exceed %d",
+               (long long)num_blocks, kTopkMaxChunks * 256);
+  if (rows == 0) return UNUM_OK;
+  UNUM_REQUIRE(num_blocks >= 1, "topk_blocks: no blocks");
+  UNUM_REQUIRE(pooled && topk_idx, "topk_blocks: null pointer");
+  const int64_t grid = (rows + 3) / 4;
+  UNUM_REQUIRE(grid <= INT32_MAX, "topk_blocks: too many rows (%lld)", (long long)rows);
+  const bool vec = (reinterpret_cast<uintptr_t>(pooled) & 15) == 0 && (row_stride % 4) == 0;
+  const int nch = static_cast<int>((num_blocks + 255) / 256);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  const int32_t NB = static_cast<int32_t>(num_blocks);
+  switch (nch) {
+#define UNUM_TOPK_ROWS_CASE(N)                                                                       \
+    case N:                                                                                          \
+      if (vec)                                                                                       \
+        hipLaunchKernelGGL((topk_rows_kernel<N, true>), g, b, 0, s, pooled, rows, row_stride, NB,    \
+                           topk_idx, topk);                                                          \
+      else                                                                                           \
+        hipLaunchKernelGGL((topk_rows_kernel<N, false>), g, b, 0, s, pooled, rows, row_stride, NB,   \
+                           topk_idx, topk);                                                          \
+      break;
+    UNUM_TOPK_ROWS_CASE(1) UNUM_TOPK_ROWS_CASE(2) UNUM_TOPK_ROWS_CASE(3) UNUM_TOPK_ROWS_CASE(4)
+    UNUM_TOPK_ROWS_CASE(5) UNUM_TOPK_ROWS_CASE(6) UNUM_TOPK_ROWS_CASE(7) UNUM_TOPK_ROWS_CASE(8)
+    UNUM_TOPK_ROWS_CASE(9) UNUM_TOPK_ROWS_CASE(10) UNUM_TOPK_ROWS_CASE(11) UNUM_TOPK_ROWS_CASE(12)
+    UNUM_TOPK_ROWS_CASE(13) UNUM_TOPK_ROWS_CASE(14) UNUM_TOPK_ROWS_CASE(15) UNUM_TOPK_ROWS_CASE(16)
+#undef UNUM_TOPK_ROWS_CASE
+    default: UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "topk_blocks: %lld blocks", (long long)num_blocks);
+  }
+  return check_launch("topk_blocks");
 }

@@ -11,7 +11,9 @@ follows from the layouts of its three ops:
    and each row is read in place (``max_pooling_1d_varlen.py:127-183``);
 3. a top-k picks the ``topk`` best 64-token blocks per (head, token), ties
    going to the lower block id (fused with step 2 in one kernel,
-   ``maxpool_topk``);
+   ``maxpool_topk``; or, when the scores are not wanted, steps 1 and 2 run
+   as one kernel, ``infllmv2_attn_stage1_maxpool``, and ``topk_blocks``
+   selects from its pooled rows);
    the ids are sorted ascending as the reference's tests sort them
    (``test/test_sparse_kernel.py:42-43``) and blocks whose pooled score is
    ``-inf`` (no compressed key in the window) become ``-1``;
@@ -29,29 +31,53 @@ import torch
 
 from . import _lib
 from ._common import as_i32, as_int, require_gpu
-from .infllm_v2 import infllmv2_attn_stage1, max_pooling_1d_varlen
+from .infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_maxpool,
+                        max_pooling_1d_varlen)
 from .sparse_kernel_extension import get_block_table
 
 FUSED_MAX_BLOCKS = 4096  # the fused pool + top-k kernel keeps a row's blocks in registers
 
 
 def topk_blocks(pooled, topk):
-    """Top-``topk`` block ids per row of ``pooled [H, T, NB]``, sorted ascending,
-    int32; among equal scores the lower id wins; ids whose score is ``-inf``
-    are ``-1``.  ``topk`` larger than ``NB`` pads with ``-1``."""
+    """Top-``topk`` block ids per row of ``pooled [H, T, NB]`` on the GPU, sorted
+    ascending, int32; among equal scores the lower id wins; ids whose score is
+    ``-inf`` are ``-1``; ``topk`` larger than ``NB`` pads with ``-1`` (first).
+
+    The selection of ``maxpool_topk`` over scores already pooled (the output of
+    ``infllmv2_attn_stage1_maxpool``): one gfx950 kernel, a row per wave, for
+    up to 4096 blocks a row.  Wider rows (past the kernel's registers) take a
+    stable descending device sort, which orders ties the same way.
+    """
+    op = "topk_blocks"
+    dev = require_gpu(op, pooled)
+    if pooled.dim() != 3:
+        raise ValueError(f"{op}: pooled must be [H, T, NB]")
+    topk = as_int(topk, "topk", op)
+    if topk < 1:
+        raise ValueError(f"{op}: topk must be >= 1, got {topk}")
     H, T, NB = pooled.shape
-    k = min(topk, NB)
-    # Neighbouring windows share a tap, so equal pooled scores are common; a
-    # stable descending sort breaks ties toward the lower block id, which makes
-    # the selection deterministic (torch.topk leaves tie order unspecified).
-    vals, idx = torch.sort(pooled, dim=-1, descending=True, stable=True)
-    vals, idx = vals[..., :k], idx[..., :k]
-    idx = torch.where(vals == float("-inf"), torch.full_like(idx, -1), idx)
-    idx = idx.sort(dim=-1).values.to(torch.int32)
-    if k < topk:
-        pad = torch.full((H, T, topk - k), -1, dtype=torch.int32, device=pooled.device)
-        idx = torch.cat([pad, idx], dim=-1)
-    return idx
+    if NB > FUSED_MAX_BLOCKS:
+        k = min(topk, NB)
+        vals, idx = torch.sort(pooled, dim=-1, descending=True, stable=True)
+        vals, idx = vals[..., :k], idx[..., :k]
+        idx = torch.where(vals == float("-inf"), torch.full_like(idx, -1), idx)
+        idx = idx.sort(dim=-1).values.to(torch.int32)
+        if k < topk:
+            pad = torch.full((H, T, topk - k), -1, dtype=torch.int32, device=dev)
+            idx = torch.cat([pad, idx], dim=-1)
+        return idx
+    x = pooled if pooled.dtype == torch.float32 else pooled.float()  # exact for bf16 / fp16
+    if x.stride(-1) != 1 or (T > 1 and x.stride(1) != NB) or (H > 1 and x.stride(0) != T * NB):
+        x = x.contiguous()
+    out = torch.empty(H, T, topk, dtype=torch.int32, device=dev)
+    if out.numel() == 0 or NB == 0:
+        return out.fill_(-1) if NB == 0 else out
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.unum_topk_blocks(_lib.ptr(x), H * T, NB, NB, _lib.ptr(out), topk,
+                                  _lib.stream_ptr(dev))
+    _lib.check(st, op)
+    return out
 
 
 def maxpool_topk(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seqlen_q, max_context_len,
@@ -129,6 +155,18 @@ def select_blocks(q, k, cu_seqlens_q, cu_seqlens_k, block_table, token_to_bs, to
     """
     op = "select_blocks"
     dev = require_gpu(op, q, k, cu_seqlens_q, cu_seqlens_k, block_table)
+    if not return_intermediates:
+        # The scores are not wanted: stage 1 pools its rows in the kernel
+        # (the score tensor never goes to HBM), then the top-k runs over the
+        # pooled rows -- the same ids as the chain below, bit for bit.
+        pooled = infllmv2_attn_stage1_maxpool(q, k, cu_seqlens_q, cu_seqlens_k, max_context_len,
+                                              max_seqlen_k=max_seqlen_k,
+                                              softmax_scale=softmax_scale, causal=causal,
+                                              local_blocks=local_blocks, init_blocks=init_blocks,
+                                              block_size=block_size, stride=stride)
+        idx = topk_blocks(pooled, topk)
+        return get_block_table(idx, block_table, token_to_bs, token_pos_in_bs, seqlen_q,
+                               head_group=head_group)
     scores = infllmv2_attn_stage1(q, k, None, cu_seqlens_q, cu_seqlens_k,
                                   max_seqlen_k=max_seqlen_k, softmax_scale=softmax_scale,
                                   causal=causal)
