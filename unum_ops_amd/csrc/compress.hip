@@ -17,8 +17,11 @@
 // head, a row of the group's lanes covering all heads and dims of a token,
 // and the wave's lane groups split the unit's windows between them.  A lane group
 // walks its consecutive windows loading and summing every half-block once
-// (16 token loads at once, the next half-block's while the current one is
-// summed): each raw key is read once.
+// (16 token loads at once, the next two or three half-blocks' while the
+// current one is summed): each raw key is read once.  A workgroup is one
+// wave, so the few hundred units of a long sequence spread over every CU
+// (four-wave workgroups left half the CUs without one: cfg5's keys 17.3 ->
+// 16.4 us with both changes, bit-identical).
 #include "common.h"
 
 namespace unum {
@@ -109,8 +112,14 @@ __host__ __device__ inline int slice_elems(int64_t H, int64_t D) {
   return H * (D / 4) <= kWave ? 4 : 8;
 }
 
+// Half-block buffers of a lane group's ring: four for 8-byte slices (three
+// half-blocks of 16 loads in flight, within the 63 a wave may have
+// outstanding), three for 16-byte slices (register space).
+template <int kSW>
+constexpr int cmp_ring() { return kSW == 4 ? 4 : 3; }
+
 template <int kStride, int kSW>
-__global__ __launch_bounds__(256) void compress_keys_kernel(CompressArgs a) {
+__global__ __launch_bounds__(kWave) void compress_keys_kernel(CompressArgs a) {
   const int64_t unit = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
   if (unit >= a.n_units) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
@@ -141,23 +150,30 @@ __global__ __launch_bounds__(256) void compress_keys_kernel(CompressArgs a) {
   uint16_t* ob = a.out + (c0 * a.H + h) * a.D + d0;
   const int64_t o_st = static_cast<int64_t>(a.H) * a.D;
   // Windows j_lo .. j_hi-1 use half-blocks j_lo .. j_hi, each loaded and
-  // summed once; two register buffers alternate, so the next half-block
-  // loads while the current one is summed.
-  typename SliceT<kSW>::type w0[kStride], w1[kStride];
+  // summed once, through a ring of kCmpRing register buffers: kCmpRing-1
+  // half-blocks load while one is summed.  Past j_hi the ring reloads j_hi,
+  // so every step issues the same loads and the compiler's wait before a
+  // sum stays a partial one.
+  constexpr int kCmpRing = cmp_ring<kSW>();
+  typename SliceT<kSW>::type w[kCmpRing][kStride];
   float hp[kSW], hn[kSW];
-  half_load<kStride, kSW>(kb, a.k_st, j_lo, w0);
-  half_load<kStride, kSW>(kb, a.k_st, j_lo + 1, w1);
-  half_sum<kStride, kSW>(w0, hp);
-  for (int64_t j = j_lo; j < j_hi; j += 2) {
-    // w1 holds half-block j+1
-    if (j + 2 <= j_hi) half_load<kStride, kSW>(kb, a.k_st, j + 2, w0);
-    half_sum<kStride, kSW>(w1, hn);
-    store_window<kSW>(ob + j * o_st, hp, hn, a.inv_kernel);
-    if (j + 1 >= j_hi) break;
-    // w0 holds half-block j+2
-    if (j + 3 <= j_hi) half_load<kStride, kSW>(kb, a.k_st, j + 3, w1);
-    half_sum<kStride, kSW>(w0, hp);
-    store_window<kSW>(ob + (j + 1) * o_st, hn, hp, a.inv_kernel);
+#pragma unroll
+  for (int r = 0; r < kCmpRing - 1; ++r) {
+    const int64_t hb = j_lo + r < j_hi ? j_lo + r : j_hi;
+    half_load<kStride, kSW>(kb, a.k_st, hb, w[r]);
+  }
+  for (int64_t base = j_lo;; base += kCmpRing) {
+#pragma unroll
+    for (int r = 0; r < kCmpRing; ++r) {
+      const int64_t hb = base + r;  // the half-block summed at this step
+      if (hb > j_hi) return;
+      const int64_t nxt = hb + kCmpRing - 1 < j_hi ? hb + kCmpRing - 1 : j_hi;
+      half_load<kStride, kSW>(kb, a.k_st, nxt, w[(r + kCmpRing - 1) % kCmpRing]);
+      half_sum<kStride, kSW>(w[r], hn);
+      if (hb > j_lo) store_window<kSW>(ob + (hb - 1) * o_st, hp, hn, a.inv_kernel);
+#pragma unroll
+      for (int e = 0; e < kSW; ++e) hp[e] = hn[e];
+    }
   }
 }
 
@@ -191,7 +207,7 @@ extern "C" int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_s
   UNUM_REQUIRE(windows_per_unit % groups == 0,
                "compress_keys: windows_per_unit=%d not a multiple of the %d lane groups",
                windows_per_unit, groups);
-  const int64_t blocks = (n_units * kWave + 255) / 256;
+  const int64_t blocks = n_units;
   UNUM_REQUIRE(blocks <= INT32_MAX, "compress_keys: too many units (%lld)", (long long)n_units);
   CompressArgs a;
   a.k = static_cast<const __bf16*>(k);
@@ -211,10 +227,10 @@ extern "C" int unum_compress_keys(const void* k, int64_t k_stride_t, int64_t k_s
   a.per_group = windows_per_unit / groups;
   a.inv_kernel = 1.0f / static_cast<float>(kernel_size);
   if (slice_elems(H, D) == 4)
-    hipLaunchKernelGGL((compress_keys_kernel<16, 4>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+    hipLaunchKernelGGL((compress_keys_kernel<16, 4>), dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
                        static_cast<hipStream_t>(stream), a);
   else
-    hipLaunchKernelGGL((compress_keys_kernel<16, 8>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+    hipLaunchKernelGGL((compress_keys_kernel<16, 8>), dim3(static_cast<unsigned>(blocks)), dim3(kWave), 0,
                        static_cast<hipStream_t>(stream), a);
   return check_launch("compress_keys");
 }
