@@ -335,6 +335,22 @@ __device__ __forceinline__ int32_t lanes_below(uint64_t mask) {
                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
 }
 
+// Inclusive sum over the wave's lanes (lane 0 first): DPP shifts within each
+// 16-lane row, then each row's total carried into the rows after it.
+template <int CTRL, int RM>
+__device__ __forceinline__ uint32_t dpp_or0(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, RM, 0xF, false));
+}
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
+  x += dpp_or0<0x111, 0xF>(x);  // row_shr:1
+  x += dpp_or0<0x112, 0xF>(x);  // row_shr:2
+  x += dpp_or0<0x114, 0xF>(x);  // row_shr:4
+  x += dpp_or0<0x118, 0xF>(x);  // row_shr:8
+  x += dpp_or0<0x142, 0xA>(x);  // row_bcast:15 into rows 1 and 3
+  x += dpp_or0<0x143, 0xC>(x);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
 // The top K of a row's keys (blocks n = 256*ch + 4*lane + e; key 0, below
 // every real key, past NB) into orow.  `list` is the wave's short list in LDS
 // (kTopkShortList keys; unused with one chunk).
@@ -348,6 +364,14 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
     for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
       for (int e = 0; e < 4; ++e) n += __popcll(__ballot(key[ch][e] >= cand));
+    return n;
+  };
+  auto count_eq = [&](uint32_t cand) -> int32_t {
+    int32_t n = 0;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) n += __popcll(__ballot(key[ch][e] == cand));
     return n;
   };
   uint32_t tau = 0;     // the K-th largest key (0 when every block is taken)
@@ -392,13 +416,8 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
         for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
           for (int e = 0; e < 4; ++e) mine += (key[ch][e] >= lo && key[ch][e] <= hi) ? 1 : 0;
-        int32_t incl = mine;  // inclusive prefix over the lanes
-#pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-          const int32_t v = __shfl_up(incl, d);
-          incl += lane >= d ? v : 0;
-        }
-        const int32_t total = __builtin_amdgcn_readfirstlane(__shfl(incl, kWave - 1));
+        const int32_t incl = static_cast<int32_t>(wave_incl_sum(static_cast<uint32_t>(mine)));
+        const int32_t total = __builtin_amdgcn_readlane(incl, kWave - 1);
         if (total <= kTopkShortList) {
           int32_t pos = incl - mine;
 #pragma unroll
@@ -442,6 +461,33 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
   lead = lead < K ? lead : K;
   for (int32_t j = lane; j < lead; j += kWave) orow[j] = -1;
   int32_t out_pos = lead, eq_seen = 0;
+  // Usually every key equal to tau is taken (ties at the threshold are rare)
+  // or none is: a key is then taken by its compares alone, without the
+  // running rank of the equal keys below.
+  if (need_eq == 0 || count_eq(tau) == need_eq) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      bool take[4];
+      uint64_t m_take[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t k = key[ch][e];
+        take[e] = (k > tau || (need_eq > 0 && k == tau)) && k != kKeyNegInf;
+        m_take[e] = __ballot(take[e]);
+      }
+      int32_t pos = out_pos;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pos += lanes_below(m_take[e]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (take[e] && pos < K) orow[pos] = 256 * ch + 4 * lane + e;
+        pos += take[e] ? 1 : 0;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out_pos += __popcll(m_take[e]);
+    }
+    return;
+  }
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     bool eq[4];
