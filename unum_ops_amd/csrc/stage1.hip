@@ -1086,17 +1086,20 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
             bool big = false;
 #pragma unroll
             for (int k = 0; k < TW; ++k) {
-#pragma unroll
-              for (int rr = 0; rr < 4; ++rr) le[k][rr] = 0.f;
+              // The quad's four exponentials per (lane, head), summed as a
+              // tree; one compare of the largest sum checks them all.
+              float e[4][4];
 #pragma unroll
               for (int u = 0; u < 4; ++u) {
-                le[k][0] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].x, c, mc[k][0]));
-                le[k][1] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].y, c, mc[k][1]));
-                le[k][2] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].z, c, mc[k][2]));
-                le[k][3] += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].w, c, mc[k][3]));
+                e[u][0] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].x, c, mc[k][0]));
+                e[u][1] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].y, c, mc[k][1]));
+                e[u][2] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].z, c, mc[k][2]));
+                e[u][3] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[k][u].w, c, mc[k][3]));
               }
 #pragma unroll
-              for (int rr = 0; rr < 4; ++rr) big |= !(le[k][rr] <= kStLimit);
+              for (int rr = 0; rr < 4; ++rr) le[k][rr] = (e[0][rr] + e[1][rr]) + (e[2][rr] + e[3][rr]);
+              const float m = fmaxf(fmaxf(le[k][0], le[k][1]), fmaxf(le[k][2], le[k][3]));
+              big |= !(m <= kStLimit);
             }
             if (__builtin_amdgcn_ballot_w64(big) != 0) {
               // Rare: a quad far above the reference.  Move the reference of
