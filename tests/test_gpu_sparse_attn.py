@@ -78,6 +78,12 @@ def test_slot_table_path_is_bit_identical(seed, dev):
     assert torch.equal(fused, table)
 
 
+@pytest.mark.parametrize("Hkv", [3, 4])
+def test_three_and_four_kv_heads(Hkv, dev):
+    # The cache row of slot s for head h is Hkv*s + h; q and out carry 16*Hkv heads.
+    _check(_problem(70 + Hkv, T=6, Hkv=Hkv, K=6), dev)
+
+
 def test_peaky_scores_and_one_kv_head(dev):
     # Large scores move the running max many times (the lazy rescale); Hkv = 1.
     _check(_problem(41, Hkv=1, kscale=6.0), dev)
