@@ -109,12 +109,6 @@ __device__ __forceinline__ float sa_sum_x32(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int N>
-__device__ __forceinline__ void sa_vm_wait() {
-  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
 __device__ __forceinline__ int lds_addr(const void* p) {
   return static_cast<int>(reinterpret_cast<uintptr_t>((sa_lds_ptr)(p)));
 }
