@@ -5,6 +5,7 @@ has a single HIP runtime: torch's).  There is no fallback: if the library is
 missing or fails to load, every op raises ``RuntimeError``.
 """
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -171,10 +172,26 @@ def check(status, what):
     raise RuntimeError(f"{what}: {msg} (status {status})")
 
 
+# torch's own raw-stream query (what its kernel launchers call): a plain int,
+# without building a Stream object per call.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device):
-    """Raw hipStream_t of torch's current stream on ``device``."""
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """Raw hipStream_t of torch's current stream on ``device`` (an int; the
+    entry points take it as ``void*``)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    """A tensor's device address for a ``void*`` argument (None: NULL)."""
+    return t.data_ptr() if t is not None else None
+
+
+def device_guard(device):
+    """``torch.cuda.device(device)``, or nothing when it is already current."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)

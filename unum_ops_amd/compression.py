@@ -96,7 +96,7 @@ def compress_keys(k, cu_seqlens_k, kernel_size=KERNEL, stride=STRIDE, plan=None)
     if plan.total == 0:
         return out, plan.cu_comp, plan.max_len
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.unum_compress_keys(
             _lib.ptr(k), k.stride(0), k.stride(1), _lib.ptr(plan.cu_raw), _lib.ptr(plan.cu_comp),
             _lib.ptr(plan.unit_prefix), plan.n_units, _lib.ptr(out), plan.B, T, plan.total, H, D,

@@ -87,7 +87,7 @@ def infllmv2_attn_stage1(q, k, v, cu_seqlens_q, cu_seqlens_k, cu_seqlens_v=None,
     if total_k == 0:
         return out.zero_()
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         # Rows over 512 keys split their keys between workgroups through a
         # small workspace (about 1 KiB per 16 rows and split); decode
         # batches run one workgroup per row and need none.
@@ -144,7 +144,7 @@ def max_pooling_1d_varlen(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seq
     if cu_k.numel() < batch + 1 or cache.numel() < batch:
         raise ValueError(f"{op}: cu_seqlens_k / cache_lens shorter than the batch ({batch})")
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.unum_max_pooling_1d_varlen(
             _lib.ptr(x), x.numel(), _POOL_DTYPES[x.dtype],
             _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(cache), _lib.ptr(out),
@@ -219,7 +219,7 @@ def infllmv2_attn_stage1_maxpool(q, k, cu_seqlens_q, cu_seqlens_k, max_context_l
     if pooled.numel() == 0:
         return (pooled, scores) if return_scores else pooled
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         # The key-split workspace of stage 1: rows over 512 keys then pool in
         # the split kernels' second pass.
         ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(

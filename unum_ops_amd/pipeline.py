@@ -73,7 +73,7 @@ def topk_blocks(pooled, topk):
     if out.numel() == 0 or NB == 0:
         return out.fill_(-1) if NB == 0 else out
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.unum_topk_blocks(_lib.ptr(x), H * T, NB, NB, _lib.ptr(out), topk,
                                   _lib.stream_ptr(dev))
     _lib.check(st, op)
@@ -126,7 +126,7 @@ def maxpool_topk(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seqlen_q, ma
     if cu_k.numel() < batch + 1 or cache.numel() < batch:
         raise ValueError(f"{op}: cu_seqlens_k / cache_lens shorter than the batch ({batch})")
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.unum_max_pooling_1d_varlen_topk(
             _lib.ptr(x), x.numel(), _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(cache),
             _lib.ptr(pooled), _lib.ptr(idx), H, n_q, batch, flat_stride, nb,

@@ -93,7 +93,7 @@ def sparse_paged_attention(query, key_cache, value_cache, num_heads, num_kv_head
             raise ValueError(f"{op}: slots must be [{T}, {Hkv}, {K * SPARSE_BLOCK}]")
         sl = as_i32(slots, "slots", op)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.unum_sparse_paged_attention(
             _lib.ptr(q), q.stride(0), q.stride(1),
             _lib.ptr(key_cache), _lib.ptr(value_cache), row_stride, n_rows,

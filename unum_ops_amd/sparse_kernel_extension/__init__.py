@@ -37,7 +37,7 @@ def _block_table(op, topk_idx, block_table, token_to_bs, token_pos_in_bs, seqlen
     if out.numel() == 0:
         return out
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         st = lib.unum_get_block_table(
             _lib.ptr(idx), idx.stride(0), idx.stride(1), idx.stride(2),
             _lib.ptr(bt), bt.stride(0), _lib.ptr(bs),
