@@ -33,7 +33,7 @@ METRIC = ("stage1 TFLOP/s (% bf16 MFMA peak); maxpool+block-table GB/s (% HBM) @
 
 
 # Components whose kernel is shorter than the Python wrapper's host time per
-# call (measured: 5.3 and 12.0 us of GPU time against 15-16 us between eager
+# call (measured: 5.3 and 12.0 us of GPU time against 11-16 us between eager
 # launches); their calls allocate with torch.empty and never sync with the
 # host, so they are captured in a HIP graph and timed without the launch gaps.
 # The other components' kernels outlast the host time per call (graph and
@@ -372,7 +372,7 @@ def main():
     log("per-kernel: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in per_op.items())
         + f"; step {wall * 1e3 / args.steps:.3f} ms")
 
-    # Kernels shorter than their Python wrapper's ~15 us of host time per call
+    # Kernels shorter than their Python wrapper's ~11 us of host time per call
     # are launch-bound when timed as above: they are timed again as a HIP
     # graph of K captured calls, replayed between two events (the GPU time of
     # K back-to-back launches); the eager figure is kept beside it.
