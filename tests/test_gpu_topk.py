@@ -82,6 +82,43 @@ def test_most_keys_between_the_bounds(dev):
     _check(d, dev, 64, **_kw(16 * 8448, 64 * 2112))
 
 
+def _list_rows(T, ties, seed):
+    """2112-block rows (nine chunks a lane) for the search over the short list:
+    lane 0's largest key, 0.1, is the lower bound; every other lane holds an
+    anchor in [0.12, 0.18]; everything else is below 0.05 but for m_r large
+    keys outside lane 0, so row r's list holds 64 + m_r keys."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.rand(1, T, 2112, generator=g) * 0.05
+    anchor = 4 * torch.arange(64)                   # block 4l: lane l, chunk 0
+    x[0, :, anchor] = 0.12 + torch.rand(T, 64, generator=g) * 0.06
+    x[0, :, 0] = 0.1
+    free = torch.arange(2112) % 256 >= 4            # lane 0 keeps 0.1 as its largest
+    free[anchor] = False
+    free_cols = torch.nonzero(free).flatten()
+    ms = []
+    for r in range(T):
+        m = min(r * 26, 1500) if r < T - 2 else 1500
+        cols = free_cols[torch.randperm(free_cols.numel(), generator=g)[:m]]
+        v = 0.2 + torch.rand(m, generator=g) * 0.8
+        if ties:
+            v = torch.floor(v * 64.0) / 64.0
+        x[0, r, cols] = v
+        ms.append(m)
+    x[0, :, 1] = float("inf")
+    return x, ms
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_short_list_of_every_length(ties, dev):
+    # Lists of 64 to 1024 keys (one to sixteen a lane) and, on the last rows,
+    # more than 1024 (the search then counts every key).
+    x, _ = _list_rows(40, ties, 31 + ties)
+    for topk in (1, 64):
+        got = topk_blocks(x.to(dev), topk)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
+
+
 def test_minus_inf_blocks_on_long_rows(dev):
     # Short key counts leave most of a 2112-block row at -inf.  With 38 or 10
     # finite blocks some lanes hold only -inf, the bounds take every key and

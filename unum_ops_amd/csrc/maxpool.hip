@@ -297,7 +297,12 @@ __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
 constexpr int kTopkMaxChunks = 16;  // NB <= 4096 (64 keys per lane)
 constexpr uint32_t kKeyNegInf = 0x007fffffu;  // order_key(-inf)
 constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)
-constexpr int kTopkShortList = 512;  // keys between the bounds kept per wave (8 a lane)
+constexpr int kTopkShortList = 1024;  // keys between the bounds kept per wave (16 a lane)
+
+// Storage of the per-wave short lists of a 256-thread block: none with one
+// chunk a row, where the search counts the keys in registers.
+template <int NCH>
+constexpr int topk_list_len() { return NCH >= 2 ? kTopkShortList : 1; }
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t b = __float_as_uint(f);
@@ -351,6 +356,42 @@ __device__ __forceinline__ uint32_t wave_incl_sum(uint32_t x) {
   return x;
 }
 
+// The threshold search over a short list of `total` keys in LDS, NS of them
+// a lane (total <= 64*NS; the slots past it hold key 0, below every
+// candidate): bits `top`..0 of tau, each kept when at least K keys (the
+// list's count plus n_inf) lie at or above the candidate, stopping at a
+// candidate past `lo` with exactly K.  Every key above the final tau is in
+// the list or +inf, and every key equal to it is in the list, so the list
+// also gives n_gt (keys > tau, with the n_inf ones) and n_eq (keys == tau).
+template <int NS>
+__device__ __forceinline__ uint32_t list_search(const uint32_t* list, int32_t total, int top,
+                                                uint32_t tau, int32_t n_inf, int32_t K,
+                                                uint32_t lo, int32_t& n_gt, int32_t& n_eq) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t sk[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int idx = i * kWave + lane;
+    sk[i] = idx < total ? list[idx] : 0u;
+  }
+  for (int bit = top; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    int32_t n = n_inf;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) n += __popcll(__ballot(sk[i] >= cand));
+    if (n >= K) tau = cand;
+    if (n == K && cand > lo) break;
+  }
+  n_gt = n_inf;
+  n_eq = 0;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    n_gt += __popcll(__ballot(sk[i] > tau));
+    n_eq += __popcll(__ballot(sk[i] == tau));
+  }
+  return tau;
+}
+
 // The top K of a row's keys (blocks n = 256*ch + 4*lane + e; key 0, below
 // every real key, past NB) into orow.  `list` is the wave's short list in LDS
 // (kTopkShortList keys; unused with one chunk).
@@ -377,6 +418,7 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
   uint32_t tau = 0;     // the K-th largest key (0 when every block is taken)
   int32_t need_eq = 0;  // blocks with key == tau to take, lowest ids first
   int32_t neg = 0;      // taken blocks scoring -inf
+  int32_t n_eq = -1;    // blocks with key == tau, when the short list counted them
   if (NB > K) {
     // Bounds on tau that fix its high bits: while fewer than K blocks are
     // forced to +inf, tau is at most the largest finite key; and for K <= 64
@@ -387,6 +429,7 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
     // save (measured, with the reductions on ds_bpermute and on DPP alike).
     int top = 31;
     bool searched = false;
+    int32_t n_gt = 0;  // keys > tau, from the short list
     const int32_t n_inf = NCH >= 2 && K <= kWave ? count_ge(kKeyPosInf) : K;
     if (n_inf < K) {
       uint32_t lmax = 0;
@@ -407,7 +450,7 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
         // Only keys in [lo, hi] (and the +inf ones, counted apart) can be at
         // or above a candidate past lo: when at most kTopkShortList of them
         // exist they go to a per-wave list in LDS, and the search counts
-        // that list -- eight keys a lane instead of 4*NCH.  At or below lo
+        // that list -- at most sixteen keys a lane instead of 4*NCH.  At or below lo
         // the list undercounts, but still holds at least 64 >= K keys, so
         // the `>= K` decision stands; only the exact-K stop waits for a
         // candidate past lo.
@@ -425,19 +468,16 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (key[ch][e] >= lo && key[ch][e] <= hi) list[pos++] = key[ch][e];
-          uint32_t sk[kTopkShortList / kWave];
-#pragma unroll
-          for (int i = 0; i < kTopkShortList / kWave; ++i) {
-            const int idx = i * kWave + lane;
-            sk[i] = idx < total ? list[idx] : 0u;  // 0 lies below every candidate
-          }
-          for (int bit = top; bit >= 0; --bit) {
-            const uint32_t cand = tau | (1u << bit);
-            int32_t n = n_inf;
-#pragma unroll
-            for (int i = 0; i < kTopkShortList / kWave; ++i) n += __popcll(__ballot(sk[i] >= cand));
-            if (n >= K) tau = cand;
-            if (n == K && cand > lo) break;
+          // Every step counts only the list's occupied slots: a search over
+          // ceil(total/64) keys a lane (cfg5's real rows: 205-701 keys).
+          switch ((total + kWave - 1) / kWave) {
+#define TOPK_NS(N) \
+  case N: tau = list_search<N>(list, total, top, tau, n_inf, K, lo, n_gt, n_eq); break;
+            TOPK_NS(1) TOPK_NS(2) TOPK_NS(3) TOPK_NS(4) TOPK_NS(5) TOPK_NS(6) TOPK_NS(7)
+            TOPK_NS(8) TOPK_NS(9) TOPK_NS(10) TOPK_NS(11) TOPK_NS(12) TOPK_NS(13) TOPK_NS(14)
+            TOPK_NS(15) TOPK_NS(16)
+#undef TOPK_NS
+            default: break;  // total >= 1: hi is a key of the list
           }
           searched = true;
         }
@@ -452,7 +492,7 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
       if (n >= K) tau = cand;
       if (n == K) break;
     }
-    need_eq = K - (tau == 0xffffffffu ? 0 : count_ge(tau + 1));
+    need_eq = K - (searched ? n_gt : tau == 0xffffffffu ? 0 : count_ge(tau + 1));
     neg = tau == kKeyNegInf ? need_eq : 0;
   } else {
     neg = count_ge(kKeyNegInf) - count_ge(kKeyNegInf + 1);
@@ -464,7 +504,7 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
   // Usually every key equal to tau is taken (ties at the threshold are rare)
   // or none is: a key is then taken by its compares alone, without the
   // running rank of the equal keys below.
-  if (need_eq == 0 || count_eq(tau) == need_eq) {
+  if (need_eq == 0 || (n_eq >= 0 ? n_eq : count_eq(tau)) == need_eq) {
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
       bool take[4];
@@ -534,7 +574,7 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   const int lane = threadIdx.x & (kWave - 1);
   const RowCtx c = row_ctx(a, row, t);
   const int32_t NB = static_cast<int32_t>(a.NB);
-  __shared__ uint32_t short_list[4][kTopkShortList];  // one per wave of the 256-thread block
+  __shared__ uint32_t short_list[4][topk_list_len<NCH>()];  // one per wave of the 256-thread block
   uint32_t key[NCH][4];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
@@ -559,7 +599,7 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* pooled, int
   if (row >= rows) return;  // wave-uniform
   const int lane = threadIdx.x & (kWave - 1);
   const float* src = pooled + row * row_stride;
-  __shared__ uint32_t short_list[4][kTopkShortList];
+  __shared__ uint32_t short_list[4][topk_list_len<NCH>()];
   uint32_t key[NCH][4];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
