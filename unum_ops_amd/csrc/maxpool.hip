@@ -501,54 +501,12 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
   lead = lead < K ? lead : K;
   for (int32_t j = lane; j < lead; j += kWave) orow[j] = -1;
   int32_t out_pos = lead, eq_seen = 0;
-  // Usually every key equal to tau is taken (ties at the threshold are rare)
-  // or none is: a key is then taken by its compares alone, without the
-  // running rank of the equal keys below.
-  if (need_eq == 0 || (n_eq >= 0 ? n_eq : count_eq(tau)) == need_eq) {
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-      bool take[4];
-      uint64_t m_take[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t k = key[ch][e];
-        take[e] = (k > tau || (need_eq > 0 && k == tau)) && k != kKeyNegInf;
-        m_take[e] = __ballot(take[e]);
-      }
-      int32_t pos = out_pos;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pos += lanes_below(m_take[e]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (take[e] && pos < K) orow[pos] = 256 * ch + 4 * lane + e;
-        pos += take[e] ? 1 : 0;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) out_pos += __popcll(m_take[e]);
-    }
-    return;
-  }
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) {
-    bool eq[4];
-    uint64_t m_eq[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      eq[e] = key[ch][e] == tau && need_eq > 0;
-      m_eq[e] = __ballot(eq[e]);
-    }
-    int32_t eq_rank = eq_seen;  // equal keys at lower block ids
-#pragma unroll
-    for (int e = 0; e < 4; ++e) eq_rank += lanes_below(m_eq[e]);
-    bool take[4];
+  // The keys of chunk ch with take[e] set go to the next output slots, in
+  // block-id order.
+  auto emit = [&](int ch, const bool (&take)[4]) {
     uint64_t m_take[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool sel = key[ch][e] > tau || (eq[e] && eq_rank < need_eq);
-      eq_rank += eq[e] ? 1 : 0;
-      take[e] = sel && key[ch][e] != kKeyNegInf;
-      m_take[e] = __ballot(take[e]);
-    }
+    for (int e = 0; e < 4; ++e) m_take[e] = __ballot(take[e]);
     int32_t pos = out_pos;
 #pragma unroll
     for (int e = 0; e < 4; ++e) pos += lanes_below(m_take[e]);
@@ -558,10 +516,54 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
       pos += take[e] ? 1 : 0;
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      out_pos += __popcll(m_take[e]);
-      eq_seen += __popcll(m_eq[e]);
+    for (int e = 0; e < 4; ++e) out_pos += __popcll(m_take[e]);
+  };
+  // Usually every key equal to tau is taken (ties at the threshold are rare)
+  // or none is: a key is then taken by its compares alone, without the
+  // running rank of the equal keys below.
+  if (need_eq == 0 || (n_eq >= 0 ? n_eq : count_eq(tau)) == need_eq) {
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      bool take[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t k = key[ch][e];
+        take[e] = (k > tau || (need_eq > 0 && k == tau)) && k != kKeyNegInf;
+      }
+      emit(ch, take);
     }
+    return;
+  }
+  // Ranked output: the equal keys are taken by ascending id, need_eq of them.
+  // A chunk holding no equal key still to rank (none at all, or need_eq
+  // taken already) takes the keys above tau by their compares alone.
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    bool eq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) eq[e] = key[ch][e] == tau;
+    bool take[4];
+    if (eq_seen >= need_eq || __ballot(eq[0] || eq[1] || eq[2] || eq[3]) == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) take[e] = key[ch][e] > tau && key[ch][e] != kKeyNegInf;
+      emit(ch, take);
+      continue;
+    }
+    uint64_t m_eq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m_eq[e] = __ballot(eq[e]);
+    int32_t eq_rank = eq_seen;  // equal keys at lower block ids
+#pragma unroll
+    for (int e = 0; e < 4; ++e) eq_rank += lanes_below(m_eq[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool sel = key[ch][e] > tau || (eq[e] && eq_rank < need_eq);
+      eq_rank += eq[e] ? 1 : 0;
+      take[e] = sel && key[ch][e] != kKeyNegInf;
+    }
+    emit(ch, take);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) eq_seen += __popcll(m_eq[e]);
   }
 }
 
