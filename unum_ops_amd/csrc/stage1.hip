@@ -1559,12 +1559,19 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
 #pragma unroll
   for (int qd = 1; qd < NQ; ++qd) {
     f32x4 sa[2], sb[2];
-    row_half_mfma(kl, 2 * qd, qf, sa);
-    row_half_mfma(kl, 2 * qd + 1, qf, sb);
     if (qd == NQ - 1) {
+      // The last quad: its second half only when a key of it is visible.
+      const bool both = vis > 64 * qd + 32;  // wave-uniform
+      row_half_mfma(kl, 2 * qd, qf, sa);
+      if (both) row_half_mfma(kl, 2 * qd + 1, qf, sb);
       row_stage_exp<true, NQ>(2 * qd, sa, c, mc, vis, sel, pw, lsum);
-      row_stage_exp<true, NQ>(2 * qd + 1, sb, c, mc, vis, sel, pw, lsum);
+      if (both)
+        row_stage_exp<true, NQ>(2 * qd + 1, sb, c, mc, vis, sel, pw, lsum);
+      else
+        pw[qd][1] = f16x8{};
     } else {
+      row_half_mfma(kl, 2 * qd, qf, sa);
+      row_half_mfma(kl, 2 * qd + 1, qf, sb);
       row_stage_exp<false, NQ>(2 * qd, sa, c, mc, vis, sel, pw, lsum);
       row_stage_exp<false, NQ>(2 * qd + 1, sb, c, mc, vis, sel, pw, lsum);
     }
