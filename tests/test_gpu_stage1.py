@@ -61,6 +61,21 @@ def test_causal_corners(q_lens, ctx, dev):
     _check(d, _run(d, dev))
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_last_quad_half_boundaries(causal, dev):
+    # Rows whose last 64-key quad ends just before, at and just after its
+    # second half (32 keys in) and its second half's second tile, for every
+    # quad count of a 512-column row: the resident kernel computes a last
+    # quad's second half only when one of its keys is visible.
+    lens = sorted({64 * qd + o for qd in range(8) for o in (1, 16, 17, 31, 32, 33, 48, 49, 63, 64)
+                   if 64 * qd + o <= 512})
+    q_lens = [3] * len(lens)
+    ctx = [16 * (L - 1) + 32 for L in lens]  # compressed to exactly L keys
+    d = workloads.stage1_inputs(q_lens, ctx, seed=97 + causal)
+    assert [int(v) for v in d["cu_seqlens_k"][1:] - d["cu_seqlens_k"][:-1]] == lens
+    _check(d, _run(d, dev, causal=causal), causal=causal)
+
+
 @pytest.mark.parametrize("peaky", [False, True])
 def test_peaky_keys(peaky, dev):
     d = workloads.stage1_inputs([128, 64], [4096, 12000], seed=11, peaky=peaky)
