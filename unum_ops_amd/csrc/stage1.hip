@@ -868,9 +868,44 @@ __device__ __forceinline__ void stream_scores(const bf16x8* buf, int qd, const S
 // its own, storing nothing, to carry that column in.
 struct Stage1Split {
   float* ws;        // [pieces][n_splits][16 rows][16 heads]
+  int32_t* pieces;  // [pieces][kPieceInts]: each piece as the first pass found it
   int32_t chunks;   // 256-key chunks per split
   int32_t n_splits;
 };
+
+// A piece as stored between the two key-split launches: the first pass's
+// split-0 workgroup of each piece writes what find_piece returned, and the
+// second pass reads it back with one load instead of searching cu_seqlens
+// again behind the first pass's traffic.
+constexpr int kPieceInts = 12;
+
+__device__ __forceinline__ void store_piece(int32_t* dst, const Piece& pc) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t v[kPieceInts] = {pc.kind, pc.b, pc.g, pc.qs, pc.lq_len, pc.ks, pc.lk, pc.t0, pc.n,
+                                 static_cast<int32_t>(pc.extra), static_cast<int32_t>(pc.n_extra), 0};
+#pragma unroll
+  for (int i = 0; i < kPieceInts; ++i)
+    if (lane == i) dst[i] = v[i];
+}
+
+__device__ __forceinline__ Piece load_piece(const int32_t* src) {
+  const i32x4 a = *reinterpret_cast<const i32x4*>(src);
+  const i32x4 b = *reinterpret_cast<const i32x4*>(src + 4);
+  const i32x4 c = *reinterpret_cast<const i32x4*>(src + 8);
+  Piece pc{};
+  pc.kind = __builtin_amdgcn_readfirstlane(a[0]);
+  pc.b = __builtin_amdgcn_readfirstlane(a[1]);
+  pc.g = __builtin_amdgcn_readfirstlane(a[2]);
+  pc.qs = __builtin_amdgcn_readfirstlane(a[3]);
+  pc.lq_len = __builtin_amdgcn_readfirstlane(b[0]);
+  pc.ks = __builtin_amdgcn_readfirstlane(b[1]);
+  pc.lk = __builtin_amdgcn_readfirstlane(b[2]);
+  pc.t0 = __builtin_amdgcn_readfirstlane(b[3]);
+  pc.n = __builtin_amdgcn_readfirstlane(c[0]);
+  pc.extra = __builtin_amdgcn_readfirstlane(c[1]);
+  pc.n_extra = __builtin_amdgcn_readfirstlane(c[2]);
+  return pc;
+}
 
 template <typename OutT, int W, int TW, int CT, int NB, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
@@ -905,7 +940,14 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 
   const int split = kSplit ? static_cast<int>(blockIdx.y) : 0;
   constexpr int kChunkKeys = CT * 16;
-  const Piece sg = find_piece(a, blockIdx.x, R);
+  Piece sg;
+  if constexpr (kSplit == 2) {
+    sg = load_piece(sp.pieces + static_cast<int64_t>(blockIdx.x) * kPieceInts);
+  } else {
+    sg = find_piece(a, blockIdx.x, R);
+    if (kSplit == 1 && split == 0 && threadIdx.x < kWave)
+      store_piece(sp.pieces + static_cast<int64_t>(blockIdx.x) * kPieceInts, sg);
+  }
   if (sg.kind == kOrphan && kSplit != 1 && split == 0) zero_orphan_rows<OutT, kPool>(a, pp, sg, W);
   if (sg.kind == kSeq) {
     const int64_t n = sg.n;
@@ -1982,8 +2024,9 @@ inline bool decode_batch(const Stage1Args& a) {
 // all against the piece bound (measured on decode batches: four left CUs
 // idle, eight and more spent more on combining the splits; pieces of 4
 // tokens measured slower);
-// the workspace holds one float per (piece, split, row, head).  A plan of
-// one split runs the whole-row kernel instead.
+// the workspace holds one float per (piece, split, row, head), then each
+// piece's kPieceInts lookup result.  A plan of one split runs the whole-row
+// kernel instead.
 struct SplitPlan {
   int64_t pieces;
   int32_t chunks, n_splits;
@@ -2002,7 +2045,9 @@ SplitPlan split_plan(int64_t Hkv, int64_t Tq, int64_t B, int64_t out_cols) {
   const int64_t n_splits = out_chunks > 0 ? (out_chunks + chunks - 1) / chunks : 0;
   p.chunks = static_cast<int32_t>(chunks);
   p.n_splits = static_cast<int32_t>(n_splits < 65535 ? n_splits : 0);
-  p.bytes = p.n_splits >= 2 ? p.pieces * p.n_splits * R * 16 * static_cast<int64_t>(sizeof(float)) : 0;
+  p.bytes = p.n_splits >= 2 ? p.pieces * (p.n_splits * R * 16 * static_cast<int64_t>(sizeof(float)) +
+                                          kPieceInts * static_cast<int64_t>(sizeof(int32_t)))
+                            : 0;
   return p;
 }
 
@@ -2012,7 +2057,11 @@ template <typename OutT, bool kPool>
 int launch_split(const Stage1Args& a, const Stage1Pool& pp, const SplitPlan& plan, void* ws,
                  hipStream_t s) {
   constexpr int kTW = kStTokensPerWave;
-  const Stage1Split sp{static_cast<float*>(ws), plan.chunks, plan.n_splits};
+  // The workspace: the split sums, then the pieces (split_plan's bytes).
+  const int64_t R = split_waves(a.Tq, a.B) * kStTokensPerWave;
+  float* sums = static_cast<float*>(ws);
+  int32_t* pieces = reinterpret_cast<int32_t*>(sums + plan.pieces * plan.n_splits * R * 16);
+  const Stage1Split sp{sums, pieces, plan.chunks, plan.n_splits};
   const dim3 grid(static_cast<unsigned>(plan.pieces), static_cast<unsigned>(plan.n_splits));
   const char* op = kPool ? "infllmv2_attn_stage1_maxpool" : "infllmv2_attn_stage1";
   if (split_waves(a.Tq, a.B) == kStSplitWavesWide) {
