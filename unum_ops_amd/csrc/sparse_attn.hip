@@ -23,10 +23,10 @@
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (keys as M, heads as N), so a
 //     lane holds four keys of one head: the online-softmax state (max, sum)
 //     is one head per lane and needs no transposes;
-//   * P^T (bf16) is, as it stands in the accumulator layout, the B operand of
-//     v_mfma_f32_16x16x16_bf16 for O^T += V^T P^T; the V rows go to a 4 KiB
-//     LDS buffer and come back as V^T fragments through ds_read_b64_tr_b16
-//     (transposing reads);
+//   * P^T, as it stands in the accumulator layout, is the B operand of
+//     v_mfma_f32_16x16x16_bf16 for O^T += V^T P^T, taken as two bf16 terms
+//     (P to about 2^-15); the V rows go to a 4 KiB LDS buffer and come back
+//     as V^T fragments through ds_read_b64_tr_b16 (transposing reads);
 //   * the running max moves only when a stage's max exceeds it by more than
 //     8 (log2 units), so the O^T rescale is rare; exponentials stay <= 2^8.
 #include "common.h"
@@ -323,16 +323,33 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
     const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(x2, c, -m_run));
     const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(x3, c, -m_run));
     l_run += (p0 + p1) + (p2 + p3);
-    const i16x4 pb = {static_cast<short>(f32_to_bf16_bits(p0)), static_cast<short>(f32_to_bf16_bits(p1)),
-                      static_cast<short>(f32_to_bf16_bits(p2)), static_cast<short>(f32_to_bf16_bits(p3))};
+    // P^T as two bf16 terms: hi = P truncated to bf16, lo = the exact residual
+    // P - hi truncated to bf16, so hi + lo carries P to about 2^-15 (one bf16
+    // P alone, 2^-9, left the numerator off the fp32 sum l_run by up to 0.2 %
+    // of the attended values' magnitude).  A byte permute packs two values'
+    // upper halves into one dword.
+    const uint32_t u0 = __float_as_uint(p0), u1 = __float_as_uint(p1);
+    const uint32_t u2 = __float_as_uint(p2), u3 = __float_as_uint(p3);
+    const uint32_t w0 = __float_as_uint(p0 - __uint_as_float(u0 & 0xffff0000u));
+    const uint32_t w1 = __float_as_uint(p1 - __uint_as_float(u1 & 0xffff0000u));
+    const uint32_t w2 = __float_as_uint(p2 - __uint_as_float(u2 & 0xffff0000u));
+    const uint32_t w3 = __float_as_uint(p3 - __uint_as_float(u3 & 0xffff0000u));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const i16x4 pb = __builtin_bit_cast(i16x4, u32x2{__builtin_amdgcn_perm(u1, u0, 0x07060302u),
+                                                     __builtin_amdgcn_perm(u3, u2, 0x07060302u)});
+    const i16x4 pl = __builtin_bit_cast(i16x4, u32x2{__builtin_amdgcn_perm(w1, w0, 0x07060302u),
+                                                     __builtin_amdgcn_perm(w3, w2, 0x07060302u)});
     // O^T += V^T P^T, one 16-dim tile at a time
     sa_lds_i16x4* vb = (sa_lds_i16x4*)(vst + vread);
+    i16x4 vf[8];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const i16x4 vf = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      vf[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (sa_lds_i16x4*)((__attribute__((address_space(3))) char*)vb + 1024 * (dt >> 1) + 512 * (dt & 1)));
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pb, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[dt], pb, o[dt], 0, 0, 0);
     }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[dt], pl, o[dt], 0, 0, 0);
   };
 
   // ---- phase 2: the stages, gathered kRing ahead into a ring of register
