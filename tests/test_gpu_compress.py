@@ -47,6 +47,19 @@ def test_head_shapes(H, D, dev):
     _check((torch.randn(sum(lengths), H, D, generator=g) * 4).to(torch.bfloat16), lengths, dev)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_batches(seed, dev):
+    # ragged batches (more than 64 sequences for some seeds), empty and short
+    # sequences, head counts and widths drawn per seed
+    rng = np.random.default_rng(700 + seed)
+    B = int(rng.integers(1, 90))
+    lengths = [int(v) for v in rng.integers(0, 3000, B)]
+    lengths = [L if rng.random() > 0.2 else int(rng.integers(0, 48)) for L in lengths]
+    H, D = [(1, 128), (2, 128), (4, 64), (2, 64)][seed % 4]
+    g = torch.Generator().manual_seed(700 + seed)
+    _check(torch.randn(sum(lengths), H, D, generator=g).to(torch.bfloat16), lengths, dev)
+
+
 def test_strided_keys(dev):
     lengths = [500, 129]
     g = torch.Generator().manual_seed(8)
