@@ -55,6 +55,24 @@ def test_random_with_negatives_clamp_and_scalars(seed, dev):
         np.testing.assert_array_equal(_run(d, dev, head_group=hg), _oracle(d, head_group=hg))
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes(seed, dev):
+    # heads, tokens, K, sequences and table widths drawn per seed; block ids
+    # past the table, -1 and other negatives, negative physical ids
+    rng = np.random.default_rng(300 + seed)
+    H, T = int(rng.integers(1, 5)), int(rng.integers(1, 300))
+    K, B, L = int(rng.integers(1, 80)), int(rng.integers(1, 70)), int(rng.integers(1, 1200))
+    g = torch.Generator().manual_seed(300 + seed)
+    d = dict(topk_idx=torch.randint(-2, L // 64 + 3, (H, T, K), generator=g, dtype=torch.int32),
+             block_table=torch.randint(-5, 1 << 22, (B, L), generator=g, dtype=torch.int32),
+             token_to_bs=torch.randint(0, B, (T,), generator=g, dtype=torch.int32),
+             token_pos_in_bs=torch.randint(0, 64 * (L // 64 + 2), (T,), generator=g,
+                                           dtype=torch.int32),
+             seqlen_q=torch.randint(0, 64 * (L // 64 + 2), (B,), generator=g, dtype=torch.int32))
+    for hg in (2, H):
+        np.testing.assert_array_equal(_run(d, dev, head_group=hg), _oracle(d, head_group=hg))
+
+
 def test_strided_topk_and_unaligned_table(dev):
     g = torch.Generator().manual_seed(7)
     H, T, K, B, L = 2, 16, 12, 3, 777
