@@ -3,8 +3,8 @@
 Each seed draws a batch of ragged sequences (empty ones included) in one of
 four regimes: rows of at most 512 keys (the LDS-resident kernel), longer rows
 (the streaming kernel, whole rows or key splits), decode batches (one or two
-new tokens per sequence: the one-workgroup-a-row kernel) and a mix.  Stage 1
-must match the oracle at atol 1e-3 / rtol 1e-2 (the bar of test_gpu_stage1),
+new tokens per sequence: the one-workgroup-a-row kernel) and a mix, with
+peaky keys and bf16 score outputs for some seeds.  Stage 1 must match the oracle at atol 1e-3 / rtol 1e-2 (the bar of test_gpu_stage1),
 and the fused stage-1 + max-pool entry must return, bit for bit, the oracle's
 max-pool of the scores it wrote.
 """
@@ -48,16 +48,22 @@ def _batch(seed):
 @pytest.mark.parametrize("seed", range(48))
 def test_random_batches(seed, dev):
     q_lens, ctx, hq, hkv, causal = _batch(seed)
-    d = workloads.stage1_inputs(q_lens, ctx, Hq=hq, Hkv=hkv, seed=seed, raw_keys=False)
-    print(f"seed {seed}: q {q_lens} ctx {ctx} Hq {hq} Hkv {hkv} causal {causal}", flush=True)
+    # every seventh seed peaky keys (x8), every fourth a bf16 score output
+    peaky, out_dtype = seed % 7 == 3, torch.bfloat16 if seed % 4 == 1 else torch.float32
+    d = workloads.stage1_inputs(q_lens, ctx, Hq=hq, Hkv=hkv, seed=seed, raw_keys=False,
+                                peaky=peaky)
+    print(f"seed {seed}: q {q_lens} ctx {ctx} Hq {hq} Hkv {hkv} causal {causal} peaky {peaky} "
+          f"{out_dtype}", flush=True)
     q, k = d["q"].to(dev), d["k"].to(dev)
     cq, ck = d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev)
     msk = max(d["max_seqlen_k"], 1)
-    out = infllmv2_attn_stage1(q, k, None, cq, ck, max_seqlen_k=msk, causal=causal)
+    out = infllmv2_attn_stage1(q, k, None, cq, ck, max_seqlen_k=msk, causal=causal,
+                               out_dtype=out_dtype)
     torch.cuda.synchronize()
+    assert out.dtype == out_dtype
     exp = oracle_stage1(d["q"], d["k"], None, d["cu_seqlens_q"], d["cu_seqlens_k"],
                         max_seqlen_k=msk, causal=causal)
-    torch.testing.assert_close(out.cpu(), exp, atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(out.float().cpu(), exp, atol=ATOL, rtol=RTOL)
 
     max_ctx = max(max(ctx), 1)
     pooled, scores = infllmv2_attn_stage1_maxpool(q, k, cq, ck, max_ctx, max_seqlen_k=msk,
