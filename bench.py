@@ -541,7 +541,10 @@ def main():
                                pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
                                bytes=nbytes, flop=flop, entries=n_ent, bound="hbm",
                                config=cfg + " (bytes: each attended K and V row gathered once "
-                                            "per token and kv head, q, out)")
+                                            "per token and kv head, q, out; where neighbouring "
+                                            "tokens select the same blocks the gathers hit the "
+                                            "L2 / MALL, so the gathered rate can exceed the HBM "
+                                            "peak: profiles/" + name + ".txt has the HBM traffic)")
 
     for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5"),
                       ("stage1_maxpool_cfg4", "stage1_cfg4")):
