@@ -48,26 +48,29 @@ def _batch(seed):
 @pytest.mark.parametrize("seed", range(48))
 def test_random_batches(seed, dev):
     q_lens, ctx, hq, hkv, causal = _batch(seed)
-    # every seventh seed peaky keys (x8), every fourth a bf16 score output
+    # every seventh seed peaky keys (x8), every fourth a bf16 score output; the
+    # softmax scale varies too (a non-positive one runs the per-row MFMA kernel)
     peaky, out_dtype = seed % 7 == 3, torch.bfloat16 if seed % 4 == 1 else torch.float32
+    scale = [None, None, 0.05, 0.3, None, -0.08, 1.0 / 64, 0.0][seed % 8]
     d = workloads.stage1_inputs(q_lens, ctx, Hq=hq, Hkv=hkv, seed=seed, raw_keys=False,
                                 peaky=peaky)
     print(f"seed {seed}: q {q_lens} ctx {ctx} Hq {hq} Hkv {hkv} causal {causal} peaky {peaky} "
-          f"{out_dtype}", flush=True)
+          f"{out_dtype} scale {scale}", flush=True)
     q, k = d["q"].to(dev), d["k"].to(dev)
     cq, ck = d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev)
     msk = max(d["max_seqlen_k"], 1)
-    out = infllmv2_attn_stage1(q, k, None, cq, ck, max_seqlen_k=msk, causal=causal,
-                               out_dtype=out_dtype)
+    out = infllmv2_attn_stage1(q, k, None, cq, ck, max_seqlen_k=msk, softmax_scale=scale,
+                               causal=causal, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert out.dtype == out_dtype
     exp = oracle_stage1(d["q"], d["k"], None, d["cu_seqlens_q"], d["cu_seqlens_k"],
-                        max_seqlen_k=msk, causal=causal)
+                        max_seqlen_k=msk, softmax_scale=scale, causal=causal)
     torch.testing.assert_close(out.float().cpu(), exp, atol=ATOL, rtol=RTOL)
 
     max_ctx = max(max(ctx), 1)
     pooled, scores = infllmv2_attn_stage1_maxpool(q, k, cq, ck, max_ctx, max_seqlen_k=msk,
-                                                  causal=causal, return_scores=True)
+                                                  softmax_scale=scale, causal=causal,
+                                                  return_scores=True)
     torch.cuda.synchronize()
     torch.testing.assert_close(scores.cpu(), exp, atol=ATOL, rtol=RTOL)
     exp_p = oracle_pool(scores.cpu(), d["cu_seqlens_q"], d["cu_seqlens_k"],
