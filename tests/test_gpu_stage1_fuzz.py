@@ -77,3 +77,19 @@ def test_random_batches(seed, dev):
                         torch.zeros(len(q_lens), dtype=torch.int32), 16 * scores.shape[-1],
                         max_ctx, 1, 1)
     np.testing.assert_array_equal(pooled.cpu().numpy(), exp_p)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_generic_shapes(seed, dev):
+    # head groups other than 16 and head dims other than 128: the generic kernel
+    q_lens, ctx, _, _, causal = _batch(4 * seed)  # rows of at most 512 keys
+    hq, hkv, D = [(32, 4, 128), (16, 1, 64), (8, 8, 128), (24, 2, 64)][seed % 4]
+    d = workloads.stage1_inputs(q_lens, ctx, Hq=hq, Hkv=hkv, D=D, seed=seed, raw_keys=False)
+    print(f"seed {seed}: q {q_lens} ctx {ctx} Hq {hq} Hkv {hkv} D {D} causal {causal}", flush=True)
+    msk = max(d["max_seqlen_k"], 1)
+    out = infllmv2_attn_stage1(d["q"].to(dev), d["k"].to(dev), None, d["cu_seqlens_q"].to(dev),
+                               d["cu_seqlens_k"].to(dev), max_seqlen_k=msk, causal=causal)
+    torch.cuda.synchronize()
+    exp = oracle_stage1(d["q"], d["k"], None, d["cu_seqlens_q"], d["cu_seqlens_k"],
+                        max_seqlen_k=msk, causal=causal)
+    torch.testing.assert_close(out.cpu(), exp, atol=ATOL, rtol=RTOL)
