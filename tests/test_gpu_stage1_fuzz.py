@@ -4,7 +4,8 @@ Each seed draws a batch of ragged sequences (empty ones included) in one of
 four regimes: rows of at most 512 keys (the LDS-resident kernel), longer rows
 (the streaming kernel, whole rows or key splits), decode batches (one or two
 new tokens per sequence: the one-workgroup-a-row kernel) and a mix, with
-peaky keys and bf16 score outputs for some seeds.  Stage 1 must match the oracle at atol 1e-3 / rtol 1e-2 (the bar of test_gpu_stage1),
+peaky keys, bf16 score outputs, other softmax scales and strided q / k for
+some seeds.  Stage 1 must match the oracle at atol 1e-3 / rtol 1e-2 (the bar of test_gpu_stage1),
 and the fused stage-1 + max-pool entry must return, bit for bit, the oracle's
 max-pool of the scores it wrote.
 """
@@ -57,6 +58,12 @@ def test_random_batches(seed, dev):
     print(f"seed {seed}: q {q_lens} ctx {ctx} Hq {hq} Hkv {hkv} causal {causal} peaky {peaky} "
           f"{out_dtype} scale {scale}", flush=True)
     q, k = d["q"].to(dev), d["k"].to(dev)
+    if seed % 6 == 5:  # rows of a wider tensor: head strides 136, token strides 136*H
+        wq = torch.zeros(q.shape[0], q.shape[1], 136, dtype=q.dtype, device=dev)
+        wk = torch.zeros(k.shape[0], k.shape[1], 136, dtype=k.dtype, device=dev)
+        wq[:, :, 8:] = q
+        wk[:, :, :128] = k
+        q, k = wq[:, :, 8:], wk[:, :, :128]
     cq, ck = d["cu_seqlens_q"].to(dev), d["cu_seqlens_k"].to(dev)
     msk = max(d["max_seqlen_k"], 1)
     out = infllmv2_attn_stage1(q, k, None, cq, ck, max_seqlen_k=msk, softmax_scale=scale,
