@@ -1,0 +1,83 @@
+"""Register and scratch budgets of the stage-1 kernels, from the compiler.
+
+Compiles ``csrc/stage1.hip`` for gfx950 with the library's own flags and
+``-Rpass-analysis=kernel-resource-usage``, and checks every kernel instance's
+per-lane scratch and waves per SIMD against the budgets the kernels are
+designed to.  A change that makes a kernel spill (or spill more), or drops
+the LDS-resident kernel below three waves per SIMD, fails here on the CPU,
+before any GPU run.  Needs ``hipcc``; runs no GPU code.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from unum_ops_amd import build
+
+SRC = os.path.join(build.HERE, "csrc", "stage1.hip")
+
+# Per-lane scratch allowed for the instances that spill (mangled-name
+# fragment -> bytes); every other instance must use none.  The spills are the
+# eight-quad rows of the LDS-resident kernel (fp32 and bf16 scores) and its
+# largest fused-pool rows: their 168 VGPRs hold the row's 64 exponentials and
+# the redo path's state, and a fourth wave per SIMD would cost more.
+SCRATCH_BUDGET = {
+    "stage1_lds_kernelIfLi8ELb0E": 12,  # fp32 scores, 8 quads
+    "stage1_lds_kernelItLi8ELb0E": 44,  # bf16 scores, 8 quads
+    "stage1_lds_kernelIfLi7ELb1E": 20,  # fused pool, 7 quads
+    "stage1_lds_kernelIfLi8ELb1E": 52,  # fused pool, 8 quads
+}
+
+
+def _hipcc():
+    return shutil.which("hipcc") or ("/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else None)
+
+
+@pytest.fixture(scope="module")
+def usage(tmp_path_factory):
+    hipcc = _hipcc()
+    if hipcc is None:
+        pytest.skip("hipcc is not installed")
+    out = tmp_path_factory.mktemp("ru") / "stage1.o"
+    cmd = [hipcc, *build.HIP_FLAGS, *build.FILE_FLAGS.get("stage1.hip", []),
+           "-Rpass-analysis=kernel-resource-usage", "--offload-device-only", "-c", SRC, "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stderr[-3000:]
+    kernels = {}
+    name = None
+    for line in r.stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            kernels[name] = {}
+            continue
+        m = re.search(r"remark:\s+(ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]|VGPRs): (\d+)", line)
+        if m and name is not None:
+            kernels[name][m.group(1).split()[0]] = int(m.group(2))
+    return kernels
+
+
+def test_every_kernel_instance_reported(usage):
+    kinds = {k: sum(1 for n in usage if k in n) for k in
+             ("stage1_lds_kernel", "stage1_stream_kernel", "stage1_decode_kernel",
+              "stage1_mfma_kernel", "stage1_generic_kernel")}
+    assert all(v > 0 for v in kinds.values()), kinds
+    assert all("ScratchSize" in v and "Occupancy" in v and "VGPRs" in v for v in usage.values())
+    # The LDS-resident kernel's largest rows are known to need more than 128 VGPRs.
+    assert max(v["VGPRs"] for n, v in usage.items() if "stage1_lds_kernel" in n) > 128
+
+
+def test_scratch_within_budget(usage):
+    over = []
+    for name, r in usage.items():
+        budget = next((b for frag, b in SCRATCH_BUDGET.items() if frag in name), 0)
+        if r["ScratchSize"] > budget:
+            over.append((name, r["ScratchSize"], budget))
+    assert not over, over
+
+
+def test_lds_kernel_keeps_three_waves_per_simd(usage):
+    low = [(n, r["Occupancy"]) for n, r in usage.items() if "stage1_lds_kernel" in n and r["Occupancy"] < 3]
+    assert not low, low
