@@ -1,12 +1,13 @@
-"""Register and scratch budgets of the stage-1 kernels, from the compiler.
+"""Register and scratch budgets of the kernels, from the compiler.
 
-Compiles ``csrc/stage1.hip`` for gfx950 with the library's own flags and
+Compiles ``csrc/*.hip`` for gfx950 with the library's own flags and
 ``-Rpass-analysis=kernel-resource-usage``, and checks every kernel instance's
-per-lane scratch and waves per SIMD against the budgets the kernels are
-designed to.  A change that makes a kernel spill (or spill more), or drops
+per-lane scratch (and, for stage 1, waves per SIMD) against the budgets the
+kernels are designed to.  A change that makes a kernel spill (or spill more), or drops
 the LDS-resident kernel below three waves per SIMD, fails here on the CPU,
 before any GPU run.  Needs ``hipcc``; runs no GPU code.
 """
+import concurrent.futures
 import os
 import re
 import shutil
@@ -35,14 +36,13 @@ def _hipcc():
     return shutil.which("hipcc") or ("/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else None)
 
 
-@pytest.fixture(scope="module")
-def usage(tmp_path_factory):
+def _resource_usage(src, out):
+    """{kernel: {"VGPRs", "ScratchSize", "Occupancy"}} of one source."""
     hipcc = _hipcc()
     if hipcc is None:
         pytest.skip("hipcc is not installed")
-    out = tmp_path_factory.mktemp("ru") / "stage1.o"
-    cmd = [hipcc, *build.HIP_FLAGS, *build.FILE_FLAGS.get("stage1.hip", []),
-           "-Rpass-analysis=kernel-resource-usage", "--offload-device-only", "-c", SRC, "-o", str(out)]
+    cmd = [hipcc, *build.HIP_FLAGS, *build.FILE_FLAGS.get(os.path.basename(src), []),
+           "-Rpass-analysis=kernel-resource-usage", "--offload-device-only", "-c", src, "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     assert r.returncode == 0, r.stderr[-3000:]
     kernels = {}
@@ -57,6 +57,33 @@ def usage(tmp_path_factory):
         if m and name is not None:
             kernels[name][m.group(1).split()[0]] = int(m.group(2))
     return kernels
+
+
+OTHER = ["sparse_attn", "maxpool", "compress", "block_table"]
+
+
+@pytest.fixture(scope="module")
+def all_usage(tmp_path_factory):
+    """Every source compiled at once (the compiles are independent)."""
+    d = tmp_path_factory.mktemp("ru")
+    names = ["stage1", *OTHER]
+    with concurrent.futures.ThreadPoolExecutor(len(names)) as ex:
+        futs = {n: ex.submit(_resource_usage, os.path.join(build.HERE, "csrc", n + ".hip"), d / (n + ".o"))
+                for n in names}
+        return {n: f.result() for n, f in futs.items()}
+
+
+@pytest.fixture(scope="module")
+def usage(all_usage):
+    return all_usage["stage1"]
+
+
+@pytest.mark.parametrize("name", OTHER)
+def test_other_kernels_use_no_scratch(name, all_usage):
+    usage = all_usage[name]
+    assert usage, name
+    spills = [(n, r["ScratchSize"]) for n, r in usage.items() if r["ScratchSize"] != 0]
+    assert not spills, spills
 
 
 def test_every_kernel_instance_reported(usage):
