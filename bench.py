@@ -38,7 +38,8 @@ METRIC = ("stage1 TFLOP/s (% bf16 MFMA peak); maxpool+block-table GB/s (% HBM) @
 # host, so they are captured in a HIP graph and timed without the launch gaps.
 # The other components' kernels outlast the host time per call (graph and
 # eager timings agree within a few percent), so they are timed eagerly.
-GRAPH_TIMED = ("block_table_cfg5_h16", "block_table_cfg4")
+GRAPH_TIMED = ("block_table_cfg5_h16", "block_table_cfg4", "ref_stage1_1024", "ref_maxpool_8192",
+               "ref_block_table_256")
 
 
 def graph_ms(fn, steps):
@@ -79,7 +80,9 @@ def parse():
                                        "stage1_peaky", "stage1_cfg5_h16", "maxpool_cfg5_h16",
                                        "block_table_cfg5_h16", "block_table_cfg4",
                                        "stage1_maxpool_cfg4", "stage2_cfg5", "stage2_cfg4",
-                                       "topk_cfg5", "select_cfg5", "copy"],
+                                       "topk_cfg5", "select_cfg5", "stage2_gather_cfg5",
+                                       "stage2_gather_cfg4", "stage1_bf16", "ref_stage1_1024",
+                                       "ref_maxpool_8192", "ref_block_table_256", "copy"],
                     default=None,
                     help="run a single kernel (profiling); 'copy' runs a plain 256 MiB device "
                          "copy, the calibration for the FETCH_SIZE / WRITE_SIZE counters")
@@ -174,6 +177,21 @@ def build_inputs(dev):
                 for _ in range(2)]
     c4["kv"] = [torch.randn(65536, 64, 2, 128, generator=gen, device=dev).to(torch.bfloat16)
                 for _ in range(2)]
+    # The reference's published benchmark shapes (largest row of each CSV):
+    # stage 1 non-causal 1024 x 1024 (benchmark/test_infllmv2_attn_stage1.py:67-75),
+    # the H=8 bf16 max-pool at seqlen 8192 (benchmark/test_max_polling_1d.py:27-56),
+    # the block table at B=256, seq 8192, top-k 96 (benchmark/test_sparse_kernel.py:41-100).
+    gp = torch.Generator(device=dev).manual_seed(3)
+    pub = dict(s1_q=torch.randn(1024, 32, 128, generator=gp, device=dev).to(torch.bfloat16),
+               s1_k=torch.randn(1024, 2, 128, generator=gp, device=dev).to(torch.bfloat16),
+               s1_cu=torch.tensor([0, 1024], dtype=torch.int32, device=dev),
+               mp_x=torch.randn(8, 8192, 16384, generator=gp, device=dev, dtype=torch.bfloat16),
+               mp_cu_q=torch.tensor([0, 8192], dtype=torch.int32, device=dev),
+               mp_cu_k=torch.tensor([0, 16384], dtype=torch.int32, device=dev),
+               mp_cache=torch.zeros(1, dtype=torch.int32, device=dev))
+    rb = workloads.reference_test_block_table(256, 8192, 96)
+    pub["bt"] = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in rb.items()}
+    c5["published"] = pub
     torch.cuda.synchronize()
     log(f"cfg4/cfg5 inputs ready ({time.time() - t0:.1f}s)")
     return s1, s1g, mp, mpg, bt, c5
@@ -194,7 +212,7 @@ def main():
     from unum_ops_amd.infllm_v2 import (infllmv2_attn_stage1, infllmv2_attn_stage1_maxpool,
                                         max_pooling_1d_varlen)
     from unum_ops_amd.pipeline import maxpool_topk, select_blocks, topk_blocks
-    from unum_ops_amd.sparse_attention import sparse_paged_attention
+    from unum_ops_amd.sparse_attention import sparse_gather_calibrate, sparse_paged_attention
     from unum_ops_amd.sparse_kernel_extension import get_block_table
 
     dev = torch.device("cuda:0")
@@ -308,6 +326,46 @@ def main():
                                       b["topk_idx"], b["block_table"], b["token_to_bs"],
                                       b["token_pos_in_bs"], b["seqlen_q"])
 
+    # The gather floor of each stage-2 selection: the same rows read once,
+    # coalesced, with no arithmetic (the roof stage 2's time is read against).
+    def op_stage2_gather_cfg5():
+        return sparse_gather_calibrate(c5["kv"][0], c5["kv"][1], 2, bt["topk_idx"],
+                                       bt["block_table"], bt["token_to_bs"],
+                                       bt["token_pos_in_bs"], bt["seqlen_q"])
+
+    def op_stage2_gather_cfg4():
+        b = c4["bt"]
+        return sparse_gather_calibrate(c4["kv"][0], c4["kv"][1], 2, b["topk_idx"],
+                                       b["block_table"], b["token_to_bs"],
+                                       b["token_pos_in_bs"], b["seqlen_q"])
+
+    # cfg3 with the reference's own storage dtype for the scores (bf16,
+    # infllmv2_attn_stage1_triton_v2.py:188-194).
+    def op_stage1_bf16():
+        return infllmv2_attn_stage1(s1g["q"], s1g["k"], None, s1g["cu_seqlens_q"],
+                                    s1g["cu_seqlens_k"], max_seqlen_k=s1g["max_seqlen_k"],
+                                    causal=True, out_dtype=torch.bfloat16)
+
+    # The shapes the reference publishes figures for (benchmark/output/
+    # Performance_*.csv, largest row of each; inputs as benchmark/*.py build
+    # them): context for reading those figures, not a target.
+    rp = c5["published"]
+
+    def op_ref_stage1_1024():
+        return infllmv2_attn_stage1(rp["s1_q"], rp["s1_k"], rp["s1_k"], rp["s1_cu"], rp["s1_cu"],
+                                    cu_seqlens_v=rp["s1_cu"], max_seqlen_q=1024,
+                                    max_seqlen_k=1024, causal=False, out_dtype=torch.bfloat16)
+
+    def op_ref_maxpool_8192():
+        return max_pooling_1d_varlen(rp["mp_x"], rp["mp_cu_q"], rp["mp_cu_k"], rp["mp_cache"],
+                                     8192, max_context_len=8192, local_blocks=32, init_blocks=1,
+                                     block_size=64, stride=16)
+
+    def op_ref_block_table_256():
+        b = rp["bt"]
+        return get_block_table(b["topk_idx"], b["block_table"], b["token_to_bs"],
+                               b["token_pos_in_bs"], b["seqlen_q"])
+
     def op_topk_pooled_cfg5():
         return topk_blocks(c5["pooled"], 64)
 
@@ -335,7 +393,12 @@ def main():
              ("block_table_cfg4", op_block_table_cfg4),
              ("stage1_maxpool_cfg4", op_stage1_maxpool_cfg4),
              ("stage2_cfg5", op_stage2_cfg5), ("stage2_cfg4", op_stage2_cfg4),
-             ("topk_cfg5", op_topk_pooled_cfg5), ("select_cfg5", op_select_cfg5)]
+             ("stage2_gather_cfg5", op_stage2_gather_cfg5),
+             ("stage2_gather_cfg4", op_stage2_gather_cfg4),
+             ("topk_cfg5", op_topk_pooled_cfg5), ("select_cfg5", op_select_cfg5),
+             ("stage1_bf16", op_stage1_bf16), ("ref_stage1_1024", op_ref_stage1_1024),
+             ("ref_maxpool_8192", op_ref_maxpool_8192),
+             ("ref_block_table_256", op_ref_block_table_256)]
     if args.only:
         ops = [o for o in ops if o[0] == args.only]
         extra = [o for o in extra if o[0] == args.only]
@@ -535,16 +598,74 @@ def main():
                                                              b["token_pos_in_bs"], b["seqlen_q"],
                                                              nseq)
             t = per_op[name] * 1e-3
-            comps[name] = dict(us=per_op[name] * 1e3, gbs=nbytes / t / 1e9,
-                               pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
-                               tflops=flop / t / 1e12,
+            comps[name] = dict(us=per_op[name] * 1e3, tflops=flop / t / 1e12,
                                pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
-                               bytes=nbytes, flop=flop, entries=n_ent, bound="hbm",
-                               config=cfg + " (bytes: each attended K and V row gathered once "
-                                            "per token and kv head, q, out; where neighbouring "
-                                            "tokens select the same blocks the gathers hit the "
-                                            "L2 / MALL, so the gathered rate can exceed the HBM "
-                                            "peak: profiles/" + name + ".txt has the HBM traffic)")
+                               gathered_gbs=nbytes / t / 1e9, bytes_gathered=nbytes, flop=flop,
+                               entries=n_ent, bound="gather",
+                               config=cfg + " (bytes_gathered: every attended K and V row once "
+                                            "per token and kv head, q, out; rows gathered by "
+                                            "neighbouring tokens hit the L2 / MALL, so "
+                                            "gathered_gbs may exceed the HBM peak -- the roof "
+                                            "is the gather floor: the same rows read with no "
+                                            "arithmetic, stage2_gather_*)")
+            floor = name.replace("stage2_", "stage2_gather_")
+            if floor in per_op:
+                comps[name].update(gather_floor_us=per_op[floor] * 1e3,
+                                   frac_of_gather_floor=per_op[floor] / per_op[name])
+    for name in ("stage2_gather_cfg5", "stage2_gather_cfg4"):
+        if name in per_op:
+            comps[name] = dict(us=per_op[name] * 1e3,
+                               config="calibration: every row " + name.replace("stage2_gather_", "")
+                                      + "'s stage 2 attends, gathered once per token and kv head "
+                                        "(coalesced, no arithmetic)")
+
+    if "stage1_bf16" in per_op:
+        flop, nbytes, _ = workloads.stage1_work(s1["cu_seqlens_q"], s1["cu_seqlens_k"], 32, 2,
+                                                128, 512, out_bytes=2)
+        t = per_op["stage1_bf16"] * 1e-3
+        comps["stage1_bf16"] = dict(us=per_op["stage1_bf16"] * 1e3, tflops=flop / t / 1e12,
+                                    pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS,
+                                    gbs=nbytes / t / 1e9,
+                                    pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS,
+                                    flop=flop, bytes=nbytes, bound="hbm",
+                                    config="cfg3 with bf16 scores (the reference's storage "
+                                           "dtype) [2,32768,512]")
+    if "ref_stage1_1024" in per_op:
+        flop, nbytes, _ = workloads.stage1_work([0, 1024], [0, 1024], 32, 2, 128, 1024,
+                                                causal=False, out_bytes=2)
+        t = per_op["ref_stage1_1024"] * 1e-3
+        comps["ref_stage1_1024"] = dict(
+            us=per_op["ref_stage1_1024"] * 1e3, tflops=flop / t / 1e12,
+            pct_bf16_mfma_peak=100 * flop / t / 1e12 / PEAK_BF16_TFLOPS, gbs=nbytes / t / 1e9,
+            pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, flop=flop, bytes=nbytes,
+            reference_published_ms={"CUDA": 0.264032, "Triton": 1.410048, "Triton_v2": 0.95744},
+            config="the reference's published stage-1 shape: seqlen_q = seqlen_k = 1024, "
+                   "non-causal, Hq32/Hkv2/D128, bf16 scores [2,1024,1024] "
+                   "(Performance_infllmv2_attn_stage1.csv:9; its GPU is not named)")
+    if "ref_maxpool_8192" in per_op:
+        nbytes = workloads.maxpool_bytes([0, 8192], [0, 16384], [0], 8, 128, elem=2)
+        t = per_op["ref_maxpool_8192"] * 1e-3
+        comps["ref_maxpool_8192"] = dict(
+            us=per_op["ref_maxpool_8192"] * 1e3, gbs=nbytes / t / 1e9,
+            pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
+            reference_published_ms={"CUDA": 0.432128, "Triton": 0.55552},
+            config="the reference's published max-pool shape: H=8, seqlen 8192, bf16 scores "
+                   "[8,8192,16384] read with row stride 512, local 32, init 1 -> [8,8192,128] "
+                   "(Performance_max_pooling_1d.csv:9; its GPU is not named)")
+    if "ref_block_table_256" in per_op:
+        b = c5["published"]["bt"]
+        nbytes = workloads.block_table_bytes(b["topk_idx"].cpu(), b["token_to_bs"].cpu(), 2, 256,
+                                             96, 256)
+        t = per_op["ref_block_table_256"] * 1e-3
+        comps["ref_block_table_256"] = dict(
+            us=per_op["ref_block_table_256"] * 1e3, gbs=nbytes / t / 1e9,
+            pct_hbm_peak=100 * nbytes / t / 1e9 / PEAK_HBM_GBS, bytes=nbytes,
+            reference_published_ms={"Torch": 0.616416, "CUDA_v3": 0.173056,
+                                    "Triton_v3": 0.116736},
+            config="the reference's published block-table shape: B=256, seq 8192, top-k 96 "
+                   "(inputs regenerated from benchmark/test_sparse_kernel.py:41-100's seeds) "
+                   "-> int32 [256,2,6144] (Performance_get_block_table.csv:7; its GPU is not "
+                   "named)")
 
     for name, src in (("stage1_maxpool", "stage1"), ("stage1_maxpool_cfg5", "stage1_cfg5"),
                       ("stage1_maxpool_cfg4", "stage1_cfg4")):
@@ -681,6 +802,33 @@ def host_cpu():
         avail = len(os.sched_getaffinity(0))
     except (AttributeError, OSError):
         avail = os.cpu_count()
+    # When the model name is generic (a VM may report just the vendor line),
+    # add lscpu's model name and the family / model / stepping numbers.
+    fms = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for row in f:
+                key, _, val = row.partition(":")
+                key = key.strip()
+                if key in ("cpu family", "model", "stepping") and key not in fms:
+                    fms[key] = val.strip()
+                if len(fms) == 3:
+                    break
+    except OSError:
+        pass
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for row in out.splitlines():
+            if row.startswith("Model name:"):
+                name = row.split(":", 1)[1].strip()
+                if name and (model is None or len(name) > len(model)):
+                    model = name
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    if fms:
+        model = f"{model or 'unknown'} (family {fms.get('cpu family', '?')}, model " \
+                f"{fms.get('model', '?')}, stepping {fms.get('stepping', '?')})"
     return {"cpu_model": model, "physical_cores": len(cores) or None, "cpus_available": avail}
 
 
@@ -695,27 +843,30 @@ def _median_time(fn, budget_s, min_runs=3):
 
 
 def cpu_baseline(s1, mp, bt):
-    """The CPU oracle -- the reference algorithm of each op restated in torch /
-    numpy (oracle/) -- on this host, median of bounded repeated runs:
+    """The CPU oracle -- the reference algorithm of each op restated in torch
+    (oracle/) -- on this host, on every thread the process may use, median of
+    bounded repeated runs:
 
-    * stage 1 (the headline unit, TFLOP/s): torch fp32 on every thread the
-      process may use, the whole cfg3 workload, about 10 s;
-    * max-pool (GB/s): the numpy restatement of the reference's Triton kernel
-      (max_pooling_1d_varlen.py:33-183; the reference has no torch version)
-      on the whole cfg2 input, one thread, at least 3 runs;
-    * block table (GB/s): the numpy restatement of get_block_table_ref_torch
-      (get_table_torch.py:4-44, same gather-then-where steps) on the whole
-      cfg5 block-table stage, one thread, at least 3 runs.
+    * stage 1 (the headline unit, TFLOP/s): torch fp32, the whole cfg3
+      workload, about 10 s;
+    * max-pool (GB/s): the torch restatement of the reference's Triton kernel
+      (max_pooling_1d_varlen.py:33-124; the reference has no torch version)
+      on the whole cfg2 input, at least 3 runs;
+    * block table (GB/s): get_block_table_ref_torch's steps in torch
+      (get_table_torch.py:4-44: block_table[bs], gather, where) on the whole
+      cfg5 block-table stage, at least 3 runs.
     """
     import torch
 
-    import oracle
+    from oracle.block_table import get_block_table_torch
+    from oracle.maxpool import max_pooling_1d_varlen_torch
     from oracle.stage1 import infllmv2_attn_stage1 as oracle_stage1
     from tests import workloads
 
     host = host_cpu()
     threads = host["cpus_available"] or os.cpu_count() or 1
     torch.set_num_threads(threads)
+    threads = torch.get_num_threads()
     flop, _, _ = workloads.stage1_work(s1["cu_seqlens_q"], s1["cu_seqlens_k"], 32, 2, 128, 512)
     oracle_stage1(s1["q"][:512], s1["k"][:511], None, torch.tensor([0, 512], dtype=torch.int32),
                   torch.tensor([0, 511], dtype=torch.int32), max_seqlen_k=511,
@@ -724,32 +875,33 @@ def cpu_baseline(s1, mp, bt):
         s1["q"], s1["k"], None, s1["cu_seqlens_q"], s1["cu_seqlens_k"],
         max_seqlen_k=s1["max_seqlen_k"], causal=True), 10)
     log(f"cpu baseline: stage 1 {med:.2f} s per cfg3 pass ({n} runs, {threads} threads)")
-    line = {"value": round(flop / med / 1e12, 5), "unit": "TFLOP/s",
-            "cores": torch.get_num_threads(), "kind": "port",
+    line = {"value": round(flop / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
             "sample": f"oracle stage 1 (torch fp32 CPU) on the whole cfg3 workload (4 x 8192 "
                       f"tokens), median of {n} runs", **host}
 
     mp_bytes = workloads.maxpool_bytes(mp["cu_seqlens_q"], mp["cu_seqlens_k"], mp["cache_lens"],
                                        2, 256)
-    med, n = _median_time(lambda: oracle.max_pooling_1d_varlen(
+    med, n = _median_time(lambda: max_pooling_1d_varlen_torch(
         mp["input"], mp["cu_seqlens_q"], mp["cu_seqlens_k"], mp["cache_lens"],
         mp["max_seqlen_q"], mp["max_context_len"], mp["local_blocks"], mp["init_blocks"]), 5)
-    log(f"cpu baseline: max-pool {med:.2f} s per cfg2 pass ({n} runs)")
-    comps = {"maxpool": {"value": round(mp_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
-                         "kind": "port",
-                         "sample": "numpy restatement of the reference's Triton max-pool "
+    log(f"cpu baseline: max-pool {med:.2f} s per cfg2 pass ({n} runs, {threads} threads)")
+    comps = {"maxpool": {"value": round(mp_bytes / med / 1e9, 3), "unit": "GB/s",
+                         "cores": threads, "kind": "port",
+                         "sample": "torch restatement of the reference's Triton max-pool "
                                    "(the reference ships no torch version) on the whole cfg2 "
                                    f"input, median of {n} runs"}}
 
     ids, table = bt["topk_idx"].cpu(), bt["block_table"].cpu()
     tok, pos, slen = bt["token_to_bs"].cpu(), bt["token_pos_in_bs"].cpu(), bt["seqlen_q"].cpu()
     bt_bytes = workloads.block_table_bytes(ids, tok, 2, 4096, 64, 1)
-    med, n = _median_time(lambda: oracle.get_block_table(ids, table, tok, pos, slen), 5)
-    log(f"cpu baseline: block table {med:.2f} s per cfg5 stage ({n} runs)")
-    comps["block_table"] = {"value": round(bt_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1,
-                            "kind": "port",
-                            "sample": "numpy restatement of get_block_table_ref_torch on the "
-                                      f"whole cfg5 block-table stage, median of {n} runs"}
+    med, n = _median_time(lambda: get_block_table_torch(ids, table, tok, pos, slen), 5)
+    log(f"cpu baseline: block table {med:.2f} s per cfg5 stage ({n} runs, {threads} threads)")
+    comps["block_table"] = {"value": round(bt_bytes / med / 1e9, 3), "unit": "GB/s",
+                            "cores": threads, "kind": "port",
+                            "sample": "get_block_table_ref_torch's steps in torch (block_table[bs], "
+                                      "gather, where) on the whole cfg5 block-table stage, "
+                                      f"median of {n} runs"}
     line["components"] = comps
     return line
 

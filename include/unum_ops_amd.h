@@ -10,6 +10,11 @@
  * Status: UNUM_OK (0) on success, a negative UNUM_ERR_* code otherwise; the
  * thread-local message of the last failure is returned by unum_last_error().
  *
+ * Devices: the stage-1 entry points plan for the current device (its CU
+ * count; the no-allocation entry its scratch array), so their `stream` must
+ * belong to the current device -- the null stream is the current device's;
+ * a stream of another device returns UNUM_ERR_INVALID_ARGUMENT.
+ *
  * Reference interfaces replaced (paths relative to Yanguan619/unum_ops):
  *   unum_infllmv2_attn_stage1  <- infllmv2_attn_stage1 =
  *       src/unum_ops/infllm_v2/infllmv2_attn_stage1_triton_v2.py:153-228
@@ -78,8 +83,11 @@ int unum_abi_version(void);
  *     length): vis is computed from the real key count, then capped at
  *     out_cols; the row is the softmax over the keys it keeps (the dropped
  *     keys are in no denominator), so it still sums to G;
- *   - key ranges of cu_seqlens_k outside [0, Tk): keys outside k read as
- *     zero; no load leaves k.
+ *   - key ranges of cu_seqlens_k outside [0, Tk): a sequence whose first
+ *     key row cu_seqlens_k[b] lies outside [0, Tk) reads none of its keys,
+ *     and keys at rows past the end of k are not read; a key not read
+ *     scores as a zero key (q . k = 0), on every kernel path.  No load
+ *     leaves k.
  * q and k must be finite: the reference maps a NaN score row to 0
  * (infllmv2_attn_stage1_triton_v2.py:227); this library is built without NaN
  * semantics, and the result for an inf or NaN input is not defined.
@@ -121,10 +129,13 @@ int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t 
  * (one per device, held until the process ends).  Its address on a device is
  * resolved on the first call there (with that device current); make that
  * first call outside graph capture.  A problem whose key split needs more
- * than 4 MiB returns UNUM_ERR_WORKSPACE without launching; the split plan
- * keeps about six workgroups per CU, which bounds its workspace near
- * 8 KiB per CU (about 2 MiB on a 256-CU MI355X), so on that GPU every
- * problem fits.  Every
+ * than 4 MiB returns UNUM_ERR_WORKSPACE without launching.  The split plan
+ * targets six workgroups per CU: pieces * splits < 6 * CUs + pieces, with
+ * fewer than 6 * CUs pieces whenever keys split, and 1 KiB per (piece,
+ * split) plus 48 bytes per piece, so the workspace stays below 12.3 KiB per
+ * CU -- 3.14 MiB on a 256-CU MI355X (3.07 MiB is the largest any problem
+ * reaches there), and the 4 MiB array holds every problem on GPUs of up to
+ * 326 CUs.  Every
  * call on one device shares that device's array: calls that overlap on one
  * device (other streams, other threads) race and must be serialised by the
  * caller.  Nothing in the array needs clearing: each call writes every
@@ -293,7 +304,8 @@ int unum_get_block_table(const int32_t* topk_idx, int64_t topk_stride_h,
  * (wrapping int32) -- lies in [0, n_rows).  Then
  *   out[t, h*G+i] = sum_j softmax_j(scale * q[t,h*G+i] . K[row_j]) V[row_j]
  * over the attended entries (repeats counted), fp32 math, and 0 when (t, h)
- * has none.  G = Hq / Hkv must be 16 and D 128; K <= 64; q, the caches and
+ * has none.  Any finite scale is accepted (zero gives the mean of the
+ * attended V rows, a negative one the softmax of the negated products).  G = Hq / Hkv must be 16 and D 128; K <= 64; q, the caches and
  * out 16-byte aligned.
  */
 int unum_sparse_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
@@ -307,6 +319,26 @@ int unum_sparse_paged_attention(const void* q, int64_t q_stride_t, int64_t q_str
                                 void* out, int32_t out_dtype, int64_t T, int64_t Hq, int64_t Hkv,
                                 int64_t D, int64_t K, int64_t B, int64_t L, float scale,
                                 void* stream);
+
+/*
+ * Gather-rate calibration for unum_sparse_paged_attention (a measurement
+ * tool; no reference counterpart).  Walks the same stages with the same
+ * table loads, row checks and K / V gathers, in the same lane pattern and
+ * pipeline depth, and does no arithmetic but an XOR of the gathered words:
+ * out, u32 [T, Hkv, 64] contiguous, receives each (t, h, lane)'s checksum.
+ * Its duration is the floor the gathers alone set for that selection, the
+ * roof against which the attention kernel's time is read.  Arguments and
+ * validation as unum_sparse_paged_attention.
+ */
+int unum_sparse_gather_calibrate(const void* key_cache, const void* value_cache,
+                                 int64_t kv_row_stride, int64_t n_rows, const int32_t* topk_idx,
+                                 int64_t topk_stride_h, int64_t topk_stride_t,
+                                 int64_t topk_stride_k, const int32_t* block_table,
+                                 int64_t bt_stride_b, const int32_t* slots,
+                                 const int32_t* token_to_bs, const int32_t* token_pos_in_bs,
+                                 int64_t pos_numel, const int32_t* seqlen_q,
+                                 int64_t seqlen_numel, uint32_t* out, int64_t T, int64_t Hkv,
+                                 int64_t K, int64_t B, int64_t L, void* stream);
 
 /*
  * Key compression: mean-pool raw keys into the compressed keys stage 1 takes.

@@ -56,6 +56,33 @@ def get_block_table(topk_idx, block_table, token_to_bs, token_pos_in_bs, seqlen_
     return np.ascontiguousarray(out.transpose(1, 0, 2))
 
 
+def get_block_table_torch(topk_idx, block_table, token_to_bs, token_pos_in_bs, seqlen_q,
+                          head_group=2):
+    """The same steps in torch ops on the CPU (every thread torch is given):
+    ``block_table[bs]``, the gather at the clamped positions and the ``where``
+    of ``get_table_torch.py:18-44``, as the benchmark's CPU baseline times
+    them.  Equal bit for bit to :func:`get_block_table`."""
+    import torch
+
+    idx = topk_idx.detach().cpu().to(torch.int32)
+    bt = block_table.detach().cpu().to(torch.int32)
+    bs = token_to_bs.detach().cpu().to(torch.int64).reshape(-1)
+    plim = token_pos_in_bs.detach().cpu().to(torch.int32).reshape(-1)
+    slen = seqlen_q.detach().cpu().to(torch.int32).reshape(-1)
+    H, T, K = idx.shape
+    L = bt.shape[1]
+    pos = (idx.unsqueeze(-1) * SPARSE_BLOCK +
+           torch.arange(SPARSE_BLOCK, dtype=torch.int32)).reshape(H, T, K * SPARSE_BLOCK)
+    seqlen = slen.expand(T) if slen.numel() == 1 else slen[bs]
+    limit = plim.expand(T) if plim.numel() == 1 else plim
+    valid = (pos >= 0) & (pos < seqlen[None, :, None]) & (pos < limit[None, :, None])
+    rows = bt[bs]                                                    # [T, L]
+    vals = torch.gather(rows.unsqueeze(0).expand(H, -1, -1), 2, pos.clamp(0, L - 1).long())
+    out = head_group * vals + torch.arange(H, dtype=torch.int32).reshape(-1, 1, 1)
+    out = torch.where(valid, out, torch.zeros((), dtype=torch.int32))
+    return out.permute(1, 0, 2).contiguous()
+
+
 def get_block_table_bruteforce(topk_idx, block_table, token_to_bs, token_pos_in_bs,
                                seqlen_q, head_group=2):
     """Scalar triple loop over (t, h, k, o) in Python ints; tiny inputs only.

@@ -102,6 +102,45 @@ def max_pooling_1d_varlen(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seq
     return out
 
 
+def max_pooling_1d_varlen_torch(input, cu_seqlens_q, cu_seqlens_k, cache_lens, max_seqlen_q,
+                                max_context_len, local_blocks, init_blocks, block_size=64,
+                                stride=16):
+    """The same restatement as :func:`max_pooling_1d_varlen` in torch ops (CPU,
+    every thread torch is given): the form the benchmark times as the CPU
+    baseline (the reference ships no torch max-pool).  Taps past the end of
+    the flat input are dropped (``oob="absent"``).  Returns float32
+    ``[H, Tq, NB]``, equal bit for bit to the numpy form."""
+    import torch
+
+    x = input.detach().cpu().float()
+    H, Tq = x.shape[0], x.shape[1]
+    NB = math.ceil(max_context_len / block_size)
+    P = block_size // stride
+    F = max_seqlen_q // stride
+    flat = x.reshape(-1)
+    numel = flat.numel()
+    lk_np, ob_np = row_params(cu_seqlens_q, cu_seqlens_k, cache_lens, Tq, block_size)
+    lk, ob = torch.from_numpy(lk_np), torch.from_numpy(ob_np)
+    n = torch.arange(NB, dtype=torch.int64)
+    ws = n * P - 1
+    force = (n[None, :] < init_blocks) | ((ob[:, None] >= n[None, :]) &
+                                          (ob[:, None] <= n[None, :] + local_blocks))
+    has_win = torch.minimum(ws[None, :] + P + 1, lk[:, None]) > ws.clamp(min=0)[None, :]
+    out = torch.empty(H, Tq, NB, dtype=torch.float32)
+    ninf = torch.tensor(-math.inf)
+    for h in range(H):
+        base = (h * Tq + torch.arange(Tq, dtype=torch.int64)) * F
+        m = torch.full((Tq, NB), -math.inf)
+        for i in range(P + 1):
+            p = ws + i
+            addr = base[:, None] + p.clamp(min=0)[None, :]
+            keep = (p[None, :] >= 0) & (p[None, :] < lk[:, None]) & (addr < numel)
+            vals = torch.where(keep, flat[addr.clamp(max=numel - 1)], ninf)
+            m = torch.fmax(m, vals)
+        out[h] = torch.where(force, torch.tensor(math.inf), torch.where(has_win, m, ninf))
+    return out
+
+
 def max_pooling_1d_varlen_bruteforce(input, cu_seqlens_q, cu_seqlens_k, cache_lens,
                                      max_seqlen_q, max_context_len, local_blocks,
                                      init_blocks, block_size=64, stride=16):

@@ -132,3 +132,34 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("UNUM_OPS_AMD_LIB", str(tmp_path / "absent.so"))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.load()
+
+
+def test_split_workspace_bound():
+    # Without a device the plan counts 256 CUs (an MI355X): the split
+    # workspace stays below 12 KiB + 288 bytes per CU, inside the 4 MiB
+    # array of the no-allocation entry, at the worst shapes (one kv head,
+    # ~24K tokens over 131072 keys).
+    lib = _lib.load()
+    worst = 0
+    for Hkv in (1, 2):
+        for B, tqs in ((1, (1, 3, 16, 300, 20000, 24021, 30000, 40000)), (8, (8, 17, 128, 2400)),
+                       (256, (256, 513, 4096, 76800))):
+            for Tq in tqs:
+                for max_k in (513, 2047, 8447, 131071, 131072):
+                    worst = max(worst, lib.unum_infllmv2_attn_stage1_workspace_size(
+                        B, Tq, 16 * Hkv, Hkv, 128, max_k))
+    assert 3 << 20 < worst < (12 * 1024 + 288) * 256 < 4 << 20, worst
+
+
+def test_stage1_checks_the_launch_device():
+    # Past validation the stage-1 entries resolve the launch device (the
+    # current one, which the stream must belong to) before any launch: with
+    # no device here they fail with a status and a message, launching nothing.
+    if torch.cuda.is_available():
+        pytest.skip("needs a host without a GPU")
+    lib = _lib.load()
+    fake = ctypes.c_void_p(256)
+    st = lib.unum_infllmv2_attn_stage1(fake, 4096, 128, fake, 256, 128, fake, fake, fake,
+                                       _lib.UNUM_DTYPE_F32, 1, 16, 16, 32, 2, 128, 16, 128,
+                                       0.08, 1, None, 0, None)
+    assert st == _lib.UNUM_ERR_LAUNCH and b"device" in lib.unum_last_error()

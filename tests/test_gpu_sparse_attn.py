@@ -150,6 +150,104 @@ def test_q_strides_and_cache_row_padding(dev):
     torch.testing.assert_close(got, oracle_attn(**p), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.05, -128 ** -0.5, 0.7])
+def test_any_scale(scale, dev):
+    # The scores are scaled before the running max and the key mask: a zero
+    # scale gives the mean of the attended V rows, a negative one the softmax
+    # of the negated products -- in partly masked stages too (-1 ids, partial
+    # blocks, the position limit).
+    p = _problem(80, T=9, K=6, neg=0.3, scale=scale)
+    p["token_pos_in_bs"][2] = 64 * 2 + 5
+    _check(p, dev)
+    _check(p, dev, out_dtype=torch.bfloat16)
+
+
+def test_misaligned_query_and_one_head_cache_slice(dev):
+    # q at an odd element offset with odd strides (copied to the kernel's
+    # layout by the wrapper), and the caches as one-head slices of two-head
+    # caches: slots s1 apart, s2 belonging to the parent.
+    p = _problem(90, T=6, Hkv=1, K=4)
+    g = torch.Generator().manual_seed(91)
+    big_q = torch.randn(6 * 17 + 1, 19, 131, generator=g).to(torch.bfloat16)
+    kc2 = torch.randn(40, 64, 2, 128, generator=g).to(torch.bfloat16)
+    vc2 = torch.randn(40, 64, 2, 128, generator=g).to(torch.bfloat16)
+    pd = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+    qd = big_q.to(dev).view(-1)[1:1 + 6 * 17 * 19 * 131].view(6, 17 * 19, 131)
+    pd["query"] = qd[:, 3:19, 2:130]
+    assert pd["query"].data_ptr() % 16 != 0
+    pd["key_cache"] = kc2.to(dev)[:, :, 1:2]
+    pd["value_cache"] = vc2.to(dev)[:, :, 1:2]
+    got = sparse_paged_attention(**pd, out_dtype=torch.float32).cpu()
+    p["query"] = pd["query"].cpu()
+    p["key_cache"], p["value_cache"] = kc2[:, :, 1:2].contiguous(), vc2[:, :, 1:2].contiguous()
+    torch.testing.assert_close(got, oracle_attn(**p), atol=ATOL, rtol=RTOL)
+
+
+def _gather_checksum(p, slots):
+    """The calibration kernel's checksum on the CPU: per (t, h, lane l =
+    16r + s), the XOR of the 32-bit words of chunk s (16 bytes) of K xor V
+    over the attended rows of keys 4r + i (i < 4) of every live stage."""
+    from oracle.sparse_attn import valid_entries
+    kc = p["key_cache"].contiguous().view(torch.int32).reshape(-1, 64).numpy()
+    vc = p["value_cache"].contiguous().view(torch.int32).reshape(-1, 64).numpy()
+    idx = p["topk_idx"].numpy().astype(np.int64)
+    Hkv, T, K = idx.shape
+    valid = valid_entries(p["topk_idx"], p["token_to_bs"], p["token_pos_in_bs"], p["seqlen_q"],
+                          p["block_table"].shape[0])
+    n_rows = kc.shape[0]
+    out = np.zeros((T, Hkv, 64), dtype=np.uint32)
+    for t in range(T):
+        for h in range(Hkv):
+            for k in range(K):
+                for q4 in range(4):
+                    e0 = 64 * k + 16 * q4
+                    p0 = ((int(idx[h, t, k]) * 64 + 16 * q4 + 2 ** 31) % 2 ** 32) - 2 ** 31
+                    if not (p0 >= 0 and _live(p, t, p0)):
+                        continue
+                    for lane in range(64):
+                        r, s = divmod(lane, 16)
+                        x = 0
+                        for i in range(4):
+                            e = e0 + 4 * r + i
+                            row = int(slots[t, h, e])
+                            if valid[t, h, e] and 0 <= row < n_rows:
+                                w = kc[row, 4 * s:4 * s + 4] ^ vc[row, 4 * s:4 * s + 4]
+                                x ^= int(np.bitwise_xor.reduce(w.astype(np.uint32)))
+                        out[t, h, lane] ^= np.uint32(x)
+    return out
+
+
+def _live(p, t, p0):
+    """Quarter starting at position p0 >= 0 of token t can hold an attended
+    entry: p0 below min(seqlen_q[b], token_pos_in_bs[t])."""
+    b = int(p["token_to_bs"][t])
+    if not 0 <= b < p["block_table"].shape[0]:
+        return False
+    sl = p["seqlen_q"].reshape(-1)
+    ps = p["token_pos_in_bs"].reshape(-1)
+    lim = min(int(sl[0] if sl.numel() == 1 else sl[b]), int(ps[0] if ps.numel() == 1 else ps[t]))
+    return p0 < lim
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_gather_calibration_checksum(seed, dev):
+    # The calibration kernel gathers exactly the rows stage 2 attends (same
+    # stages, row checks and lane pattern): its checksum equals the CPU's.
+    from unum_ops_amd.sparse_attention import sparse_gather_calibrate
+    p = _problem(110 + seed, T=5, K=5, neg=0.2)
+    p["token_pos_in_bs"][1] = 64 + 7
+    pd = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+    slots = get_block_table(pd["topk_idx"], pd["block_table"], pd["token_to_bs"],
+                            pd["token_pos_in_bs"], pd["seqlen_q"], head_group=2)
+    exp = _gather_checksum(p, slots.cpu().numpy())
+    for sl in (None, slots):
+        got = sparse_gather_calibrate(pd["key_cache"], pd["value_cache"], 2, pd["topk_idx"],
+                                      pd["block_table"], pd["token_to_bs"],
+                                      pd["token_pos_in_bs"], pd["seqlen_q"], slots=sl)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), exp)
+
+
 def _pipeline_case(p, dev, n_pages_pool, seed, check_tokens):
     """Stage 1 -> max-pool -> top-64 on the GPU for the block ids, then stage 2
     over random paged K/V caches; the oracle checks `check_tokens`."""

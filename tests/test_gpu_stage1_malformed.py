@@ -11,9 +11,11 @@
   so no key is read (they read as zero, a uniform softmax: G/vis per column)
   and nothing outside k is touched.
 
-Each case runs every MFMA kernel family: the LDS-resident kernel (at most 512
-columns), the key-streaming kernels (whole rows and key splits) and the
-decode kernel (at most two new tokens per sequence).
+Each case runs every kernel family: the LDS-resident kernel (at most 512
+columns), the key-streaming kernels (whole rows and key splits), the decode
+kernel (at most two new tokens per sequence), the row-MFMA kernel (a
+non-positive scale) and the generic kernel (four heads per group, or a q
+whose base is not 16-byte aligned).
 """
 
 import ctypes
@@ -29,43 +31,56 @@ from unum_ops_amd import _lib
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 1e-3, 1e-2
-G = 16
+SCALE = 128 ** -0.5
 
-# (q_lens, real key counts, max_seqlen_k given, key-split workspace): the
-# column count round_up(max_seqlen_k, 128) and the workspace pick the kernel.
+# (q_lens, real key counts, max_seqlen_k given, key-split workspace, query
+# heads (two kv heads), scale, q offset in elements): the column count
+# round_up(max_seqlen_k, 128), the workspace, the head count, the sign of the
+# scale and the alignment of q pick the kernel.
 CASES = {
-    "lds": ([40, 300], [700, 200], 300, False),            # 384 columns, 700 real keys
-    "stream_split": ([64, 64], [3000, 900], 1000, True),   # 1024 columns
-    "stream_whole": ([64, 64], [3000, 900], 1000, False),  # no workspace: whole rows
-    "decode": ([1, 2, 1], [3000, 2500, 800], 1000, False),  # Tq <= 2B, <= 4096 columns
+    "lds": ([40, 300], [700, 200], 300, False, 32, SCALE, 0),            # 384 columns, 700 keys
+    "stream_split": ([64, 64], [3000, 900], 1000, True, 32, SCALE, 0),   # 1024 columns
+    "stream_whole": ([64, 64], [3000, 900], 1000, False, 32, SCALE, 0),  # no workspace
+    "decode": ([1, 2, 1], [3000, 2500, 800], 1000, False, 32, SCALE, 0),  # Tq <= 2B
+    "row_mfma": ([40, 300], [700, 200], 300, False, 32, -SCALE, 0),      # non-positive scale
+    "generic_g4": ([40, 70], [700, 200], 300, False, 8, SCALE, 0),       # 4 heads per group
+    "generic_unaligned": ([40, 70], [700, 200], 300, False, 32, SCALE, 1),  # q base + 2 bytes
 }
 
 
-def _inputs(q_lens, k_lens, seed, zero_keys=False):
+def _inputs(q_lens, k_lens, seed, zero_keys=False, hq=32):
     g = torch.Generator().manual_seed(seed)
     Tq, Tk = sum(q_lens), sum(k_lens)
-    q = torch.randn(Tq, 32, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(Tq, hq, 128, generator=g).to(torch.bfloat16)
     k = torch.randn(Tk, 2, 128, generator=g).mul(0.25).to(torch.bfloat16)
     if zero_keys:
         k.zero_()
     return q, k, workloads.prefix(q_lens), workloads.prefix(k_lens)
 
 
-def _run(q, k, cu_q, cu_k, max_k, with_ws, dev):
+def _run(q, k, cu_q, cu_k, max_k, with_ws, dev, scale=SCALE, q_offset=0):
     """Stage 1 through the C entry point (NaN-filled output, so an unwritten
-    element shows), with or without the key-split workspace."""
-    q, k, cu_q, cu_k = q.to(dev), k.to(dev), cu_q.to(dev), cu_k.to(dev)
+    element shows), with or without the key-split workspace; q_offset > 0
+    places q that many elements past a 16-byte boundary."""
+    hq = q.shape[1]
+    if q_offset:
+        buf = torch.empty(q.numel() + q_offset, dtype=q.dtype, device=dev)
+        qd = buf[q_offset:].view(q.shape)
+        qd.copy_(q.to(dev))
+    else:
+        qd = q.to(dev)
+    k, cu_q, cu_k = k.to(dev), cu_q.to(dev), cu_k.to(dev)
     B = cu_q.numel() - 1
     cols = (max_k + 127) // 128 * 128
     lib = _lib.load()
-    ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(B, q.shape[0], 32, 2, 128, max_k)
+    ws_bytes = lib.unum_infllmv2_attn_stage1_workspace_size(B, qd.shape[0], hq, 2, 128, max_k)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if with_ws else None
-    out = torch.full((2, q.shape[0], cols), float("nan"), device=dev)
+    out = torch.full((2, qd.shape[0], cols), float("nan"), device=dev)
     st = lib.unum_infllmv2_attn_stage1(
-        _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
+        _lib.ptr(qd), qd.stride(0), qd.stride(1), _lib.ptr(k), k.stride(0), k.stride(1),
         _lib.ptr(cu_q), _lib.ptr(cu_k), _lib.ptr(out), _lib.UNUM_DTYPE_F32,
-        B, q.shape[0], k.shape[0], 32, 2, 128, max_k, cols,
-        ctypes.c_float(128 ** -0.5), 1, _lib.ptr(ws), ws_bytes if with_ws else 0,
+        B, qd.shape[0], k.shape[0], hq, 2, 128, max_k, cols,
+        ctypes.c_float(scale), 1, _lib.ptr(ws), ws_bytes if with_ws else 0,
         _lib.stream_ptr(dev))
     _lib.check(st, "stage1")
     torch.cuda.synchronize()
@@ -82,9 +97,10 @@ def _capped_vis(q_lens, k_lens, cols):
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_keys_past_columns_dropped_closed_form(case, dev):
-    q_lens, k_lens, max_k, ws = CASES[case]
-    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=1, zero_keys=True)
-    out = _run(q, k, cu_q, cu_k, max_k, ws, dev)
+    q_lens, k_lens, max_k, ws, hq, scale, qo = CASES[case]
+    G = hq // 2
+    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=1, zero_keys=True, hq=hq)
+    out = _run(q, k, cu_q, cu_k, max_k, ws, dev, scale, qo)
     cols = out.shape[-1]
     vis = _capped_vis(q_lens, k_lens, cols)
     j = np.arange(cols)[None, :]
@@ -95,11 +111,12 @@ def test_keys_past_columns_dropped_closed_form(case, dev):
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_keys_past_columns_dropped_oracle(case, dev):
-    q_lens, k_lens, max_k, ws = CASES[case]
-    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=2)
-    out = _run(q, k, cu_q, cu_k, max_k, ws, dev)
+    q_lens, k_lens, max_k, ws, hq, scale, qo = CASES[case]
+    G = hq // 2
+    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=2, hq=hq)
+    out = _run(q, k, cu_q, cu_k, max_k, ws, dev, scale, qo)
     exp = oracle_stage1(q, k, None, cu_q, cu_k, max_seqlen_k=max_k, causal=True,
-                        drop_past_cols=True)
+                        drop_past_cols=True, softmax_scale=scale)
     torch.testing.assert_close(out, exp, atol=ATOL, rtol=RTOL)
     vis = _capped_vis(q_lens, k_lens, out.shape[-1])
     sums = out.double().sum(-1).numpy()
@@ -109,13 +126,14 @@ def test_keys_past_columns_dropped_oracle(case, dev):
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_negative_first_key_offset_reads_nothing(case, dev):
-    q_lens, k_lens, max_k, ws = CASES[case]
-    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=3)
+    q_lens, k_lens, max_k, ws, hq, scale, qo = CASES[case]
+    G = hq // 2
+    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=3, hq=hq)
     # Sequence 0 claims keys [-5, cu_k[1]): its start lies before k.
     cu_k = cu_k.clone()
     cu_k[0] = -5
     lens = [int(cu_k[1] - cu_k[0])] + list(k_lens[1:])
-    out = _run(q, k, cu_q, cu_k, max_k, ws, dev)
+    out = _run(q, k, cu_q, cu_k, max_k, ws, dev, scale, qo)
     cols = out.shape[-1]
     # Sequence 0: every key reads as zero -> G / vis over its visible columns.
     vis0 = np.minimum(visible_counts(np.arange(q_lens[0]), q_lens[0], lens[0]), cols)
@@ -125,5 +143,21 @@ def test_negative_first_key_offset_reads_nothing(case, dev):
         np.testing.assert_allclose(out[g, :q_lens[0]].numpy(), exp0, atol=ATOL, rtol=RTOL)
     # The other sequences are unaffected.
     exp = oracle_stage1(q, k, None, cu_q, cu_k.clamp(min=0), max_seqlen_k=max_k, causal=True,
-                        drop_past_cols=True)
+                        drop_past_cols=True, softmax_scale=scale)
     torch.testing.assert_close(out[:, q_lens[0]:], exp[:, q_lens[0]:], atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("case", ["lds", "stream_split", "decode", "row_mfma", "generic_g4"])
+def test_keys_past_the_end_of_k_read_as_zero(case, dev):
+    # The last sequence claims more keys than k holds: its keys at rows past
+    # the end of k score as zero keys, on every path alike.  The oracle gets
+    # the same keys with zero rows appended.
+    q_lens, k_lens, max_k, ws, hq, scale, qo = CASES[case]
+    q, k, cu_q, cu_k = _inputs(q_lens, k_lens, seed=4, hq=hq)
+    short = k_lens[-1] // 3
+    k_cut = k[:k.shape[0] - short]
+    out = _run(q, k_cut, cu_q, cu_k, max_k, ws, dev, scale, qo)
+    k_zero = torch.cat([k_cut, torch.zeros(short, 2, 128, dtype=k.dtype)])
+    exp = oracle_stage1(q, k_zero, None, cu_q, cu_k, max_seqlen_k=max_k, causal=True,
+                        drop_past_cols=True, softmax_scale=scale)
+    torch.testing.assert_close(out, exp, atol=ATOL, rtol=RTOL)

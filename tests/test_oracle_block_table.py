@@ -97,3 +97,19 @@ def test_torch_inputs_accepted():
     assert out.shape == (4, 2, 16 * 64)
     heads = np.broadcast_to(np.arange(2)[None, :, None], out.shape)
     assert np.all(out[out != 0] % 2 == heads[out != 0])
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("scalar_pos,scalar_len", [(False, False), (True, True)])
+def test_torch_form_matches(seed, scalar_pos, scalar_len):
+    # the torch form the benchmark times as its CPU baseline gives the same ints
+    import torch
+    from oracle.block_table import get_block_table_torch
+    args = _rand_case(40 + seed, scalar_pos=scalar_pos, scalar_len=scalar_len)
+    got = get_block_table_torch(*(torch.from_numpy(a) for a in args))
+    np.testing.assert_array_equal(got.numpy(), get_block_table(*args))
+    wrap = (np.array([[[2 ** 25 + 3, -1]]], np.int32), np.arange(10, dtype=np.int32)[None, :],
+            np.array([0], np.int32), np.array([2 ** 31 - 1], np.int32),
+            np.array([2 ** 31 - 1], np.int32))
+    np.testing.assert_array_equal(get_block_table_torch(*(torch.from_numpy(a) for a in wrap)).numpy(),
+                                  get_block_table(*wrap))

@@ -131,3 +131,17 @@ def test_cfg2_shapes_and_forcing():
         for n in range(16):
             if n <= ob <= n + 1 or n == 0:
                 assert np.all(out[:, t, n] == np.inf)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_torch_form_matches(case):
+    # the torch form the benchmark times as its CPU baseline is bit-exact
+    from oracle.maxpool import max_pooling_1d_varlen_torch
+    q_lens, k_lens, cache, Fs, msq, mcl, local, init = case
+    d = workloads.maxpool_inputs(q_lens, F=Fs, H=2, seed=5, k_lens=k_lens, cache=cache)
+    x = torch.randn(d["input"].shape, generator=torch.Generator().manual_seed(9))
+    exp = max_pooling_1d_varlen(x, d["cu_seqlens_q"], d["cu_seqlens_k"], d["cache_lens"],
+                                msq, mcl, local, init, oob="absent")
+    got = max_pooling_1d_varlen_torch(x, d["cu_seqlens_q"], d["cu_seqlens_k"], d["cache_lens"],
+                                      msq, mcl, local, init)
+    np.testing.assert_array_equal(got.numpy(), exp)

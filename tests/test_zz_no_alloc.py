@@ -94,14 +94,22 @@ def test_noalloc_paths_without_split(dev):
 
 
 def test_split_plan_fits_the_array(dev):
-    # The split plan keeps about six workgroups per CU, so its workspace is
-    # bounded by the CU count (about 2 MiB at 256 CUs): every problem fits
-    # the 4 MiB array on this GPU, so the refusal past it never fires here.
+    # The split plan targets six workgroups per CU: its workspace stays below
+    # 12 KiB + 288 bytes per CU (3.14 MiB at 256 CUs; the worst problem, one
+    # kv head and ~24K tokens over 131072 keys, reaches 3.07 MiB), so every
+    # problem fits the 4 MiB array on this GPU and the refusal past it never
+    # fires here.
     lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
     worst = 0
-    for B in (1, 2, 8, 64, 256):
-        for Tq in (B, 2 * B + 1, 16 * B, 64 * B, 300 * B):
-            for max_k in (513, 700, 1000, 2047, 4095, 8447, 30000, 131071):
-                worst = max(worst, lib.unum_infllmv2_attn_stage1_workspace_size(
-                    B, Tq, 32, 2, 128, max_k))
-    assert 0 < worst <= SCRATCH_BYTES, worst
+    for Hkv in (1, 2):
+        for B in (1, 2, 8, 64, 256):
+            tqs = [B, 2 * B + 1, 16 * B, 64 * B, 300 * B]
+            if B == 1:
+                tqs += [20000, 24021, 30000, 40000]
+            for Tq in tqs:
+                for max_k in (513, 700, 1000, 2047, 4095, 8447, 30000, 131071, 131072):
+                    worst = max(worst, lib.unum_infllmv2_attn_stage1_workspace_size(
+                        B, Tq, 16 * Hkv, Hkv, 128, max_k))
+    assert 0 < worst < (12 * 1024 + 288) * cus, worst
+    assert worst <= SCRATCH_BYTES, worst

@@ -115,6 +115,17 @@ SIGNATURES = {
         ctypes.c_float,            # scale
         _p,                        # stream
     ]),
+    "unum_sparse_gather_calibrate": (ctypes.c_int, [
+        _p, _p, _i64, _i64,        # key_cache, value_cache, kv_row_stride, n_rows
+        _p, _i64, _i64, _i64,      # topk_idx + strides (h, t, k)
+        _p, _i64,                  # block_table, row stride
+        _p,                        # slots (may be NULL)
+        _p, _p, _i64,              # token_to_bs, token_pos_in_bs, numel
+        _p, _i64,                  # seqlen_q, numel
+        _p,                        # out (u32 [T, Hkv, 64])
+        _i64, _i64, _i64, _i64, _i64,  # T, Hkv, K, B, L
+        _p,                        # stream
+    ]),
     "unum_get_block_table": (ctypes.c_int, [
         _p, _i64, _i64, _i64,      # topk_idx + strides (h, t, k)
         _p, _i64,                  # block_table, row stride

@@ -47,13 +47,36 @@ __device__ __forceinline__ float wave_shr1(float v, float fill) {
                                                     0xF, 0xF, false));
 }
 
-// Compute units of the current device (cached per device; 256 if the query
-// fails).  The cache is read and written by any host thread that launches:
-// relaxed atomics make that race-free (every writer stores the same value).
-inline int num_cus() {
+// The device the launch runs on, for the entry points whose plan depends
+// on it (CU count, per-device scratch): the current device, which `stream`
+// must belong to (the null stream is the current device's).  Sets *dev and
+// returns UNUM_OK, or returns UNUM_ERR_INVALID_ARGUMENT (the stream is
+// another device's) / UNUM_ERR_LAUNCH (no usable device) with the error set.
+inline int launch_device(void* stream, const char* op, int* dev) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess || cur < 0)
+    UNUM_FAIL(UNUM_ERR_LAUNCH, "%s: no usable current device (%s)", op, hipGetErrorString(e));
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess)
+      UNUM_FAIL(UNUM_ERR_LAUNCH, "%s: hipStreamGetDevice failed: %s", op, hipGetErrorString(e));
+    if (sdev != cur)
+      UNUM_FAIL(UNUM_ERR_INVALID_ARGUMENT,
+                "%s: the stream belongs to device %d, the current device is %d (make the "
+                "stream's device current)", op, sdev, cur);
+  }
+  *dev = cur;
+  return UNUM_OK;
+}
+
+// Compute units of device `dev` (cached per device; 256 if the query fails).
+// The cache is read and written by any host thread that launches: relaxed
+// atomics make that race-free (every writer stores the same value).
+inline int num_cus(int dev) {
   static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (dev < 0 || dev >= 64) return 256;
   int n = cached[dev].load(std::memory_order_relaxed);
   if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
@@ -61,6 +84,13 @@ inline int num_cus() {
     cached[dev].store(n, std::memory_order_relaxed);
   }
   return n;
+}
+
+// Compute units of the current device.
+inline int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  return num_cus(dev);
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -15,14 +15,21 @@
 // NPU paged-attention operator (test/test_pa.py:48-71); this is its
 // arithmetic on the slots the table lists.
 //
-// One wave per (t, h).  Phase 1 stages the row of each of the K*64 entries
-// (or -1) in LDS and marks which 16-key stages hold an attended entry.
-// Phase 2 gathers each such stage's 16 K rows and 16 V rows (8 KiB) into
-// registers, kRing stages ahead of the one being computed (ordinary loads,
-// so the compiler's waits are exact).  Per stage:
+// One wave per (t, h).  The block ids give, with no table access, which
+// 16-key stages (a quarter of a 64-entry block) can hold an attended entry:
+// a quarter is live when its first position lies in [0, lim).  Each live
+// stage then takes three loads in flight, kRing stages apart: the 64 bytes
+// of the table that name its 16 rows, its 16 K rows and 16 V rows (8 KiB;
+// ordinary loads, so the compiler's waits are exact), and its arithmetic.
+// No per-entry table is kept in LDS (a wave uses a 4 KiB V buffer); the
+// launch sets the LDS per workgroup to hold eight waves per CU, the
+// occupancy at which the gathers, which bound the kernel, ran fastest.
+// Per stage:
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (keys as M, heads as N), so a
 //     lane holds four keys of one head: the online-softmax state (max, sum)
 //     is one head per lane and needs no transposes;
+//   * the scores are scaled before the max and the key mask, so any scale
+//     (zero and negative ones too) gives the softmax of the scaled scores;
 //   * P^T, as it stands in the accumulator layout, is the B operand of
 //     v_mfma_f32_16x16x16_bf16 for O^T += V^T P^T, taken as two bf16 terms
 //     (P to about 2^-15); the V rows go to a 4 KiB LDS buffer and come back
@@ -38,16 +45,22 @@ constexpr float kSaLog2e = 1.4426950408889634f;
 constexpr int kSaD = 128;          // head dim
 constexpr int kSaG = 16;           // query heads per kv head
 constexpr int kSaStageKeys = 16;   // keys per pipeline stage
-// Stages gathered ahead (register sets of 32 VGPRs).  Two, three and four
-// measured the same on the cfg4 and cfg5 selections (351 / 1840 us); six,
-// at one wave per SIMD, measured slower on cfg4 (620 against 422 us).
+// Stages in flight per wave (register sets of 33 VGPRs).
 constexpr int kSaRing = 3;
-constexpr int kSaMaxEntries = 4096;                         // K*64, K <= 64
+// LDS each workgroup (one wave) takes, the 4 KiB V buffer included: 20 KiB
+// holds a CU at eight waves.  The gathers bound the kernel and their rate
+// depends on how many waves share a CU's caches; measured on the cfg5 / cfg4
+// selections with the gather calibration below and this kernel: 12 waves per
+// CU (the register limit) 1960 / 323 us, 8 waves 1835 / 322 us, 6 waves
+// 2055 / 322 us, 5 and 4 waves 1884 / 560 us.
+constexpr int kSaLdsBytes = 20 * 1024;
+constexpr int kSaVBytes = kSaStageKeys * kSaD * 2;  // a stage's V rows
+constexpr int kSaMaxBlocks = 64;   // K <= 64 (one block id per lane)
 constexpr float kSaRescale = 8.f;  // lazy-rescale threshold (log2 units)
 
 // 256 zero bytes: the K and V "row" of every entry that is not attended, so
 // each stage issues the same loads (masked keys then score 0 and carry P = 0
-// against a V of zeros).
+// against a V of zeros); also the table "entries" of a stage past the last.
 __device__ __align__(256) uint32_t sa_zero_row[64];
 
 struct SaArgs {
@@ -66,28 +79,13 @@ struct SaArgs {
   const int32_t* pos;
   const int32_t* slen;
   int32_t pos_n, slen_n;
-  void* out;           // [T, Hkv*16, 128] contiguous
+  void* out;           // [T, Hkv*16, 128] contiguous (u32 [T, Hkv, 64] for the gather calibration)
   int32_t T, Hkv, K, B, L;
   float c;             // softmax scale * log2(e)
 };
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* sa_lds_ptr;
 typedef __attribute__((address_space(3))) i16x4 sa_lds_i16x4;
-
-// Global-to-LDS load of 4 bytes per lane at `addr` (a 256-byte run per
-// instruction), written at M0 + 4*lane.  Issued from inline assembly so that
-// the compiler inserts no wait per load: all of them are in flight at once
-// and the kernel waits once, with vmcnt(0).
-__device__ __forceinline__ void sa_dma4(uint64_t addr, int m0) {
-  int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(m0), "v"(addr)
-      : "memory");
-}
 
 // Max / sum of v over the lanes l and l^16 (l^32): v_permlane16_swap
 // (v_permlane32_swap) with v in both operands returns each lane's value and
@@ -109,8 +107,75 @@ __device__ __forceinline__ float sa_sum_x32(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ int lds_addr(const void* p) {
-  return static_cast<int>(reinterpret_cast<uintptr_t>((sa_lds_ptr)(p)));
+// The selection of one (t, h): lane k holds block id k (-1 past K), the
+// position limit min(seqlen_q[b], token_pos_in_bs[t]) (0 when t has no
+// sequence), and the base of the table the rows come from -- the slot
+// table's (t, h) row, or block_table's row b.
+struct SaSel {
+  int32_t lane_id;
+  int32_t lim;
+  int32_t h;
+  const int32_t* tab;
+};
+
+// The live stages: bit k of mq set when quarter q of block k (positions
+// p0 .. p0+15, p0 = id*64 + 16q wrapping int32) can hold an attended entry,
+// i.e. p0 lies in [0, lim).  p0 is a multiple of 16, so p0 >= 0 puts every
+// position of the quarter in [0, 2^31) and p0 < 0 puts none there.  Four
+// scalar words, not an array, so that no index into them is a runtime value.
+struct SaStages {
+  uint64_t m0, m1, m2, m3;
+};
+
+__device__ __forceinline__ SaStages sa_live(const SaSel& sel) {
+  const uint32_t base = static_cast<uint32_t>(sel.lane_id) * 64u;
+  auto live = [&](uint32_t q) {
+    const int32_t p0 = static_cast<int32_t>(base + 16u * q);
+    return p0 >= 0 && p0 < sel.lim;
+  };
+  return SaStages{__ballot(live(0)), __ballot(live(1)), __ballot(live(2)), __ballot(live(3))};
+}
+
+// The next live stage, 4k + q, in ascending order (-1 if none); clears it.
+__device__ __forceinline__ int sa_pop(SaStages& m) {
+  const uint64_t any = m.m0 | m.m1 | m.m2 | m.m3;
+  if (any == 0) return -1;
+  const int k = __builtin_ctzll(any);
+  const uint64_t bit = 1ull << k;
+  if (m.m0 & bit) { m.m0 &= ~bit; return 4 * k; }
+  if (m.m1 & bit) { m.m1 &= ~bit; return 4 * k + 1; }
+  if (m.m2 & bit) { m.m2 &= ~bit; return 4 * k + 2; }
+  m.m3 &= ~bit;
+  return 4 * k + 3;
+}
+
+// Position of this lane's entry of stage sg (lane l: entry 16q + l%16 of
+// block k), wrapping int32.
+__device__ __forceinline__ int32_t sa_pos(const SaSel& sel, int sg) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t id = __builtin_amdgcn_readlane(sel.lane_id, sg >> 2);
+  return static_cast<int32_t>(static_cast<uint32_t>(id) * 64u +
+                              static_cast<uint32_t>(16 * (sg & 3) + (lane & 15)));
+}
+
+// The table entry naming this lane's row of stage sg: the slot table's
+// entry, or block_table[b, min(max(p, 0), L-1)] (the clamp only matters for
+// entries that are not attended or at p >= L); the zero row past the last
+// stage.  One 64-byte run per stage (lanes l and l+16 read the same word).
+template <bool kTable>
+__device__ __forceinline__ int32_t sa_table(const SaArgs& a, const SaSel& sel, int sg) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t* p;
+  if (sg < 0) {
+    p = reinterpret_cast<const int32_t*>(sa_zero_row);
+  } else if constexpr (kTable) {
+    p = sel.tab + 16 * sg + (lane & 15);  // entry 64k + 16q + l%16
+  } else {
+    int32_t pc = sa_pos(sel, sg);
+    pc = pc < 0 ? 0 : (pc > a.L - 1 ? a.L - 1 : pc);
+    p = sel.tab + pc;
+  }
+  return *p;
 }
 
 // A stage in flight: this lane's K and V chunks of its key (lane l gathers
@@ -123,15 +188,24 @@ struct SaStage {
   uint32_t mask;
 };
 
-// Issue the gathers of stage `sg` (ordinary loads: the compiler waits for
-// each stage's loads exactly where they are used).  A key that is not
-// attended gathers the zero row, and so does every key when sg < 0 (no
-// stage left): every call issues the same eight loads, so on every path
-// through the ring the same number of loads follows each set and the
-// compiler's wait before using a set stays a partial one.
-__device__ __forceinline__ void sa_issue(const SaArgs& a, const int32_t* srow, int sg, SaStage& st) {
+// Issue the gathers of stage sg, whose table entry for this lane is `tv`
+// (ordinary loads: the compiler waits for each stage's loads exactly where
+// they are used).  A key that is not attended -- position at or past the
+// limit, row outside the cache -- gathers the zero row, and so does every
+// key when sg < 0 (no stage left): every call issues the same eight loads,
+// so on every path through the ring the same number of loads follows each
+// set and the compiler's wait before using a set stays a partial one.
+template <bool kTable>
+__device__ __forceinline__ void sa_issue(const SaArgs& a, const SaSel& sel, int sg, int32_t tv,
+                                         SaStage& st) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int32_t row = sg >= 0 ? srow[kSaStageKeys * sg + (lane & 15)] : -1;
+  int32_t row = -1;
+  if (sg >= 0) {
+    const int32_t r = kTable ? tv
+                             : static_cast<int32_t>(static_cast<uint32_t>(a.Hkv) * static_cast<uint32_t>(tv) +
+                                                    static_cast<uint32_t>(sel.h));
+    row = sa_pos(sel, sg) < sel.lim && r >= 0 && r < a.n_rows ? r : -1;  // the stage is live: p >= 0
+  }
   const uint64_t col = static_cast<uint64_t>(16 * (lane >> 4));
   const char *kp, *vp;
   if (row >= 0) {
@@ -148,19 +222,67 @@ __device__ __forceinline__ void sa_issue(const SaArgs& a, const int32_t* srow, i
   st.mask = static_cast<uint32_t>(__ballot(row >= 0) & 0xFFFFull);
 }
 
-// The stages to compute: a 256-bit mask in four scalar words (separate
-// variables, not an array, so that no index into it is a runtime value).
-struct SaStages {
-  uint64_t w0, w1, w2, w3;
-};
+// The (t, h) selection of this workgroup: block ids one per lane (one load,
+// complete before the ring's loads are issued), the limit and the table row.
+template <bool kTable>
+__device__ __forceinline__ SaSel sa_select(const SaArgs& a, int t, int h) {
+  const int lane = threadIdx.x & (kWave - 1);
+  SaSel sel;
+  sel.h = h;
+  sel.lim = 0;
+  sel.tab = nullptr;
+  const int32_t b = a.tok_bs[t];
+  if (b >= 0 && b < a.B) {
+    const int32_t sl = a.slen[a.slen_n == 1 ? 0 : b];
+    const int32_t ps = a.pos[a.pos_n == 1 ? 0 : t];
+    sel.lim = sl < ps ? sl : ps;  // <= 0: nothing is attended
+    sel.tab = kTable ? a.slots + (static_cast<int64_t>(t) * a.Hkv + h) * (static_cast<int64_t>(a.K) * 64)
+                     : a.bt + static_cast<int64_t>(b) * a.bt_sb;
+  }
+  const int32_t* idx_t = a.idx + static_cast<int64_t>(h) * a.i_sh + static_cast<int64_t>(t) * a.i_st;
+  sel.lane_id = lane < a.K && sel.tab != nullptr ? idx_t[static_cast<int64_t>(lane) * a.i_sk] : -1;
+  return sel;
+}
 
-// Lowest set stage of the mask (-1 if none); clears it.
-__device__ __forceinline__ int sa_pop(SaStages& m) {
-  if (m.w0) { const int b = __builtin_ctzll(m.w0); m.w0 &= m.w0 - 1; return b; }
-  if (m.w1) { const int b = __builtin_ctzll(m.w1); m.w1 &= m.w1 - 1; return 64 + b; }
-  if (m.w2) { const int b = __builtin_ctzll(m.w2); m.w2 &= m.w2 - 1; return 128 + b; }
-  if (m.w3) { const int b = __builtin_ctzll(m.w3); m.w3 &= m.w3 - 1; return 192 + b; }
-  return -1;
+// The pipeline shared by the attention kernel and the gather calibration:
+// slot j of a ring of kRing holds the gathers of stage sr[j] and the table
+// entry of the stage after it in that slot, st[j].  Every step computes the
+// oldest stage, issues the gathers of the stage whose table entry has
+// arrived and loads the table entry kRing stages further on, so a table load
+// leads its gathers, and the gathers their arithmetic, by kRing stages.  The
+// stages are walked in order, so the first slot left empty ends the walk.
+template <bool kTable, int kRing, typename Compute>
+__device__ __forceinline__ void sa_walk(const SaArgs& a, const SaSel& sel, SaStages stages,
+                                        Compute&& compute) {
+  SaStage r[kRing];
+  int sr[kRing], st[kRing];
+  int32_t tv[kRing];
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    st[j] = sa_pop(stages);
+    tv[j] = sa_table<kTable>(a, sel, st[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    sr[j] = st[j];
+    sa_issue<kTable>(a, sel, sr[j], tv[j], r[j]);
+    st[j] = sa_pop(stages);
+    tv[j] = sa_table<kTable>(a, sel, st[j]);
+  }
+  for (bool more = true; more;) {
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) {
+      if (more && sr[j] >= 0) {
+        compute(r[j]);
+        sr[j] = st[j];
+        sa_issue<kTable>(a, sel, sr[j], tv[j], r[j]);
+        st[j] = sa_pop(stages);
+        tv[j] = sa_table<kTable>(a, sel, st[j]);
+      } else {
+        more = false;
+      }
+    }
+  }
 }
 
 template <typename OutT>
@@ -178,73 +300,10 @@ __device__ __forceinline__ void sa_store4<uint16_t>(uint16_t* p, f32x4 v) {
 
 template <typename OutT, bool kTable, int kRing>
 __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
-  __shared__ int32_t srow[kSaMaxEntries];                         // 16 KiB
-  __shared__ __align__(16) char vst[kSaStageKeys * kSaD * 2];     // 4 KiB: a stage's V rows
+  __shared__ __align__(16) char vst[kSaVBytes];
   const int lane = threadIdx.x;
   const int t = blockIdx.x, h = blockIdx.y;
-  const int n_entries = a.K * 64;
-
-  const int32_t b = a.tok_bs[t];
-  const bool tok_ok = b >= 0 && b < a.B;
-  int32_t lim = 0;
-  if (tok_ok) {
-    const int32_t sl = a.slen[a.slen_n == 1 ? 0 : b];
-    const int32_t ps = a.pos[a.pos_n == 1 ? 0 : t];
-    lim = sl < ps ? sl : ps;
-  }
-
-  // ---- phase 1: the row of every entry (or -1), and the stages to compute.
-  // The 64 table values of each block -- slot-table entries, or the block
-  // table's entries at the block's positions (clamped into the row; the
-  // clamp only matters for entries that are not attended or at p >= L) --
-  // are gathered into srow by global-to-LDS loads, all in flight at once,
-  // then turned into rows in place.
-  SaStages stages{0, 0, 0, 0};
-  const int32_t* idx_t = a.idx + static_cast<int64_t>(h) * a.i_sh + static_cast<int64_t>(t) * a.i_st;
-  const int srow_m0 = __builtin_amdgcn_readfirstlane(lds_addr(srow));
-  // Lane k holds block id k: one load, complete before the gathers below are
-  // issued (a load of the compiler's inside their loop would make it wait
-  // for every gather issued before it).
-  int32_t lane_id = lane < a.K ? idx_t[static_cast<int64_t>(lane) * a.i_sk] : -1;
-  asm volatile("" : "+v"(lane_id));
-  if (tok_ok) {
-    if constexpr (kTable) {
-      const int32_t* src = a.slots + (static_cast<int64_t>(t) * a.Hkv + h) * n_entries + lane;
-      for (int k = 0; k < a.K; ++k)
-        sa_dma4(reinterpret_cast<uint64_t>(src + 64 * k), srow_m0 + 256 * k);
-    } else {
-      const int32_t* btr = a.bt + static_cast<int64_t>(b) * a.bt_sb;
-      for (int k = 0; k < a.K; ++k) {
-        const int32_t id = __builtin_amdgcn_readlane(lane_id, k);
-        int32_t pc = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(lane));
-        pc = pc < 0 ? 0 : (pc > a.L - 1 ? a.L - 1 : pc);
-        sa_dma4(reinterpret_cast<uint64_t>(btr + pc), srow_m0 + 256 * k);
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    for (int k = 0; k < a.K; ++k) {
-      const int32_t id = __builtin_amdgcn_readlane(lane_id, k);
-      const int32_t p = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(lane));
-      const int32_t v = srow[64 * k + lane];
-      const int32_t row = kTable ? v
-                                 : static_cast<int32_t>(static_cast<uint32_t>(a.Hkv) * static_cast<uint32_t>(v) +
-                                                        static_cast<uint32_t>(h));
-      const bool ok = p >= 0 && p < lim && row >= 0 && row < a.n_rows;
-      srow[64 * k + lane] = ok ? row : -1;
-      // Block k holds stages 4k .. 4k+3: bit q4 of its nibble marks a stage
-      // with an attended entry.
-      const uint64_t m = __ballot(ok);
-      uint64_t nib = 0;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) nib |= ((m >> (16 * q4)) & 0xFFFFull) ? (1ull << q4) : 0ull;
-      nib <<= 4 * (k & 15);
-      const int w = k >> 4;  // wave-uniform
-      stages.w0 |= w == 0 ? nib : 0ull;
-      stages.w1 |= w == 1 ? nib : 0ull;
-      stages.w2 |= w == 2 ? nib : 0ull;
-      stages.w3 |= w == 3 ? nib : 0ull;
-    }
-  }
+  const SaSel sel = sa_select<kTable>(a, t, h);
 
   // Query fragments, the B operand of S^T = K Q^T: lane (head n, g) holds
   // q[t, 16h + n, 32cc + 8g .. +8].
@@ -255,16 +314,15 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) qf[cc] = *reinterpret_cast<const bf16x8*>(qp + 32 * cc);
   }
-  // The compiler's own loads (the queries, phase 1) complete here, before the
-  // ring's loads are issued: it does not count those, and a wait of its own
-  // placed inside the loop would drain the ring on every stage.
+  // The compiler's own loads (ids, queries) complete here, before the ring's
+  // loads are issued: a wait of its own for them placed inside the loop would
+  // drain the ring on every stage.
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc) asm volatile("" : : "v"(qf[cc]));
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  asm volatile("" : : "v"(sel.lane_id));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const SaStages stages = sa_live(sel);
 
-  // ---- phase 2: the pipelined stages.  fifo[0..2] are the stages in flight,
-  // oldest first; the oldest is in ring buffer `slot`, the next ones follow
-  // cyclically.
   // Per-lane constants of the stage computation.
   const int g = lane >> 4;
   // V chunk i of this lane's key goes to byte 1024*i + vput of vst, which
@@ -278,7 +336,7 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
   const int vbit = (s >> 1) & 1;
   const int vread = 256 * vbit + 16 * (vkey ^ (4 * vbit)) + 8 * (s & 1);
 
-  float m_run = -INFINITY;  // c * running max of this lane's head
+  float m_run = -INFINITY;  // running max of this lane's head's scaled scores
   float l_run = 0.f;        // sum of exp2 against it over this lane's keys
   f32x4 o[8];
 #pragma unroll
@@ -286,14 +344,16 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
   const float c = a.c;
 
   auto compute = [&](const SaStage& st) {
+    if (st.mask == 0) return;  // every row of the stage outside the cache (wave-uniform)
     // V rows to LDS for the transposing reads
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<bf16x8*>(vst + 1024 * i + vput) = st.v[i];
-    // scores S^T (keys 4g + r of the stage, head lane%16)
+    // scores S^T (keys 4g + r of the stage, head lane%16), scaled first: the
+    // max and the exponentials below then hold for any sign of the scale
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.k[cc], qf[cc], acc, 0, 0, 0);
-    float x0 = acc.x, x1 = acc.y, x2 = acc.z, x3 = acc.w;
+    float x0 = acc.x * c, x1 = acc.y * c, x2 = acc.z * c, x3 = acc.w * c;
     if (st.mask != 0xFFFFu) {  // keys of the stage not attended -> -inf (wave-uniform test)
       const uint32_t mb = st.mask >> (4 * g);
       x0 = (mb & 1u) ? x0 : -INFINITY;
@@ -302,10 +362,9 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
       x3 = (mb & 8u) ? x3 : -INFINITY;
     }
     float mx = fmaxf(fmaxf(x0, x1), fmaxf(x2, x3));
-    mx = sa_max_x32(sa_max_x16(mx));
-    const float mxc = mx * c;  // every head has an attended key in the stage
-    if (__ballot(mxc > m_run + kSaRescale) != 0) {
-      const float m_new = fmaxf(m_run, mxc);
+    mx = sa_max_x32(sa_max_x16(mx));  // finite: the stage has an attended key
+    if (__ballot(mx > m_run + kSaRescale) != 0) {
+      const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
@@ -318,10 +377,10 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
       m_run = m_new;
     }
     // exponentials (0 for -inf scores); m_run is finite after the first stage
-    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, c, -m_run));
-    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, c, -m_run));
-    const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(x2, c, -m_run));
-    const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(x3, c, -m_run));
+    const float p0 = __builtin_amdgcn_exp2f(x0 - m_run);
+    const float p1 = __builtin_amdgcn_exp2f(x1 - m_run);
+    const float p2 = __builtin_amdgcn_exp2f(x2 - m_run);
+    const float p3 = __builtin_amdgcn_exp2f(x3 - m_run);
     l_run += (p0 + p1) + (p2 + p3);
     // P^T as two bf16 terms: hi = P truncated to bf16, lo = the exact residual
     // P - hi truncated to bf16, so hi + lo carries P to about 2^-15 (one bf16
@@ -351,30 +410,8 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf[dt], pl, o[dt], 0, 0, 0);
   };
+  sa_walk<kTable, kRing>(a, sel, stages, compute);
 
-  // ---- phase 2: the stages, gathered kRing ahead into a ring of register
-  // sets (indices known at compile time: the loop over the ring is
-  // unrolled); the ring is walked in order and so are the stages, so the
-  // first set left empty ends the walk.
-  SaStage r[kRing];
-  int sr[kRing];
-#pragma unroll
-  for (int j = 0; j < kRing; ++j) {
-    sr[j] = sa_pop(stages);
-    sa_issue(a, srow, sr[j], r[j]);
-  }
-  for (bool more = true; more;) {
-#pragma unroll
-    for (int j = 0; j < kRing; ++j) {
-      if (more && sr[j] >= 0) {
-        compute(r[j]);
-        sr[j] = sa_pop(stages);
-        sa_issue(a, srow, sr[j], r[j]);
-      } else {
-        more = false;
-      }
-    }
-  }
   // ---- normalise and store: lane (head n, g) holds dims 16dt + 4g + r
   const float l_tot = sa_sum_x32(sa_sum_x16(l_run));
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -389,6 +426,174 @@ __global__ __launch_bounds__(kWave) void sparse_attn_kernel(SaArgs a) {
     v.w *= inv;
     sa_store4<OutT>(orow + 16 * dt, v);
   }
+}
+
+// Calibration of the gather rate (a measurement tool, not part of the
+// attention): the same live stages, table entries and row checks, with every
+// attended K and V row read once, coalesced -- lane l = 16r + s reads the
+// 16-byte chunk s of the rows of keys 4r + i (i < 4), so 16 lanes read one
+// 256-byte row -- kRing stages in flight, and no arithmetic but an XOR of
+// the gathered words into a checksum, written per (t, h, lane) to a u32
+// [T, Hkv, 64] output.  Its time is the floor the gathers alone set for a
+// selection (the coalesced pattern measured 5 % faster than the attention
+// kernel's fragment-order gathers on cfg5, at the same eight waves per CU).
+struct SaRows {
+  i32x4 k[4];
+  i32x4 v[4];
+};
+
+// Table entries of keys 4r + i of stage sg (r = lane/16).
+template <bool kTable>
+__device__ __forceinline__ void sa_co_table(const SaArgs& a, const SaSel& sel, int sg, int32_t (&tv)[4]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int o = 4 * (lane >> 4) + i;  // entry of the quarter
+    const int32_t* p;
+    if (sg < 0) {
+      p = reinterpret_cast<const int32_t*>(sa_zero_row);
+    } else if constexpr (kTable) {
+      p = sel.tab + 16 * sg + o;
+    } else {
+      const int32_t id = __builtin_amdgcn_readlane(sel.lane_id, sg >> 2);
+      int32_t pc = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u + static_cast<uint32_t>(16 * (sg & 3) + o));
+      pc = pc < 0 ? 0 : (pc > a.L - 1 ? a.L - 1 : pc);
+      p = sel.tab + pc;
+    }
+    tv[i] = *p;
+  }
+}
+
+template <bool kTable>
+__device__ __forceinline__ void sa_co_issue(const SaArgs& a, const SaSel& sel, int sg,
+                                            const int32_t (&tv)[4], SaRows& st) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint64_t col = static_cast<uint64_t>(16 * (lane & 15));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int32_t row = -1;
+    if (sg >= 0) {
+      const int32_t id = __builtin_amdgcn_readlane(sel.lane_id, sg >> 2);
+      const int32_t p = static_cast<int32_t>(static_cast<uint32_t>(id) * 64u +
+                                             static_cast<uint32_t>(16 * (sg & 3) + 4 * (lane >> 4) + i));
+      const int32_t r = kTable ? tv[i]
+                               : static_cast<int32_t>(static_cast<uint32_t>(a.Hkv) * static_cast<uint32_t>(tv[i]) +
+                                                      static_cast<uint32_t>(sel.h));
+      row = p < sel.lim && r >= 0 && r < a.n_rows ? r : -1;
+    }
+    const char *kp, *vp;
+    if (row >= 0) {
+      const uint64_t off = static_cast<uint64_t>(row) * static_cast<uint64_t>(a.row_bytes) + col;
+      kp = a.kc + off;
+      vp = a.vc + off;
+    } else {
+      kp = vp = reinterpret_cast<const char*>(sa_zero_row) + col;
+    }
+    st.k[i] = *reinterpret_cast<const i32x4*>(kp);
+    st.v[i] = *reinterpret_cast<const i32x4*>(vp);
+  }
+}
+
+template <bool kTable, int kRing>
+__global__ __launch_bounds__(kWave) void sparse_gather_kernel(SaArgs a) {
+  const int lane = threadIdx.x;
+  const int t = blockIdx.x, h = blockIdx.y;
+  const SaSel sel = sa_select<kTable>(a, t, h);
+  asm volatile("" : : "v"(sel.lane_id));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  SaStages stages = sa_live(sel);
+  uint32_t x = 0;
+  SaRows r[kRing];
+  int sr[kRing], st[kRing];
+  int32_t tv[kRing][4];
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    st[j] = sa_pop(stages);
+    sa_co_table<kTable>(a, sel, st[j], tv[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kRing; ++j) {
+    sr[j] = st[j];
+    sa_co_issue<kTable>(a, sel, sr[j], tv[j], r[j]);
+    st[j] = sa_pop(stages);
+    sa_co_table<kTable>(a, sel, st[j], tv[j]);
+  }
+  for (bool more = true; more;) {
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) {
+      if (more && sr[j] >= 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const i32x4 kv = r[j].k[i] ^ r[j].v[i];
+          x ^= static_cast<uint32_t>(kv.x ^ kv.y ^ kv.z ^ kv.w);
+        }
+        sr[j] = st[j];
+        sa_co_issue<kTable>(a, sel, sr[j], tv[j], r[j]);
+        st[j] = sa_pop(stages);
+        sa_co_table<kTable>(a, sel, st[j], tv[j]);
+      } else {
+        more = false;
+      }
+    }
+  }
+  static_cast<uint32_t*>(a.out)[(static_cast<int64_t>(t) * a.Hkv + h) * kWave + lane] = x;
+}
+
+}  // namespace
+}  // namespace unum
+
+namespace unum {
+namespace {
+
+// Validation and argument block shared by the attention entry point and the
+// gather calibration (q, out and the scale are set by the caller).
+int sa_args(SaArgs& a, const char* op, const void* key_cache, const void* value_cache,
+            int64_t kv_row_stride, int64_t n_rows, const int32_t* topk_idx, int64_t topk_stride_h,
+            int64_t topk_stride_t, int64_t topk_stride_k, const int32_t* block_table,
+            int64_t bt_stride_b, const int32_t* slots, const int32_t* token_to_bs,
+            const int32_t* token_pos_in_bs, int64_t pos_numel, const int32_t* seqlen_q,
+            int64_t seqlen_numel, int64_t T, int64_t Hkv, int64_t K, int64_t B, int64_t L) {
+  UNUM_REQUIRE(K <= kSaMaxBlocks, "%s: at most %d blocks per token (K=%lld)", op, kSaMaxBlocks,
+               (long long)K);
+  UNUM_REQUIRE(key_cache && value_cache && topk_idx && token_to_bs && token_pos_in_bs && seqlen_q,
+               "%s: null pointer", op);
+  UNUM_REQUIRE(slots || (block_table && B >= 1 && L >= 1),
+               "%s: a block table (B, L >= 1) or a slot table is required", op);
+  UNUM_REQUIRE(pos_numel == 1 || pos_numel == T, "%s: token_pos_in_bs has %lld entries (T=%lld)",
+               op, (long long)pos_numel, (long long)T);
+  UNUM_REQUIRE(seqlen_numel == 1 || seqlen_numel >= B, "%s: seqlen_q has %lld entries (B=%lld)", op,
+               (long long)seqlen_numel, (long long)B);
+  UNUM_REQUIRE(n_rows >= 0 && kv_row_stride >= kSaD && (kv_row_stride % 8) == 0,
+               "%s: cache rows must be D elements or more apart, in multiples of 8 (stride %lld)",
+               op, (long long)kv_row_stride);
+  UNUM_REQUIRE((reinterpret_cast<uintptr_t>(key_cache) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(value_cache) & 15) == 0,
+               "%s: the caches must be 16-byte aligned", op);
+  UNUM_REQUIRE(T <= INT32_MAX && Hkv <= 65535 && n_rows <= INT32_MAX && B <= INT32_MAX &&
+                   L <= INT32_MAX,
+               "%s: size exceeds the kernel's index range", op);
+  a.kc = static_cast<const char*>(key_cache);
+  a.vc = static_cast<const char*>(value_cache);
+  a.row_bytes = kv_row_stride * 2;
+  a.n_rows = n_rows;
+  a.idx = topk_idx;
+  a.i_sh = topk_stride_h;
+  a.i_st = topk_stride_t;
+  a.i_sk = topk_stride_k;
+  a.bt = block_table;
+  a.bt_sb = bt_stride_b;
+  a.slots = slots;
+  a.tok_bs = token_to_bs;
+  a.pos = token_pos_in_bs;
+  a.slen = seqlen_q;
+  a.pos_n = static_cast<int32_t>(pos_numel);
+  a.slen_n = static_cast<int32_t>(seqlen_numel == 1 ? 1 : 2);
+  a.T = static_cast<int32_t>(T);
+  a.Hkv = static_cast<int32_t>(Hkv);
+  a.K = static_cast<int32_t>(K);
+  a.B = static_cast<int32_t>(B);
+  a.L = static_cast<int32_t>(L);
+  return UNUM_OK;
 }
 
 }  // namespace
@@ -414,61 +619,28 @@ extern "C" int unum_sparse_paged_attention(
   if (Hq != kSaG * Hkv || D != kSaD)
     UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "%s: needs 16 query heads per kv head and D = 128 (got Hq=%lld, "
               "Hkv=%lld, D=%lld)", op, (long long)Hq, (long long)Hkv, (long long)D);
-  UNUM_REQUIRE(K <= kSaMaxEntries / 64, "%s: at most %d blocks per token (K=%lld)", op,
-               kSaMaxEntries / 64, (long long)K);
-  UNUM_REQUIRE(q && key_cache && value_cache && topk_idx && token_to_bs && token_pos_in_bs &&
-                   seqlen_q && out,
-               "%s: null pointer", op);
-  UNUM_REQUIRE(slots || (block_table && B >= 1 && L >= 1),
-               "%s: a block table (B, L >= 1) or a slot table is required", op);
-  UNUM_REQUIRE(pos_numel == 1 || pos_numel == T, "%s: token_pos_in_bs has %lld entries (T=%lld)",
-               op, (long long)pos_numel, (long long)T);
-  UNUM_REQUIRE(seqlen_numel == 1 || seqlen_numel >= B, "%s: seqlen_q has %lld entries (B=%lld)", op,
-               (long long)seqlen_numel, (long long)B);
-  UNUM_REQUIRE(n_rows >= 0 && kv_row_stride >= D && (kv_row_stride % 8) == 0,
-               "%s: cache rows must be D elements or more apart, in multiples of 8 (stride %lld)",
-               op, (long long)kv_row_stride);
+  UNUM_REQUIRE(q && out, "%s: null pointer", op);
   UNUM_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (q_stride_t % 8) == 0 &&
-                   (q_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(key_cache) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(value_cache) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(out) & 15) == 0,
-               "%s: q, the caches and out must be 16-byte aligned", op);
-  UNUM_REQUIRE(T <= INT32_MAX && Hkv <= 65535 && n_rows <= INT32_MAX && B <= INT32_MAX &&
-                   L <= INT32_MAX,
-               "%s: size exceeds the kernel's index range", op);
+                   (q_stride_h % 8) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "%s: q and out must be 16-byte aligned (q strides multiples of 8)", op);
+  UNUM_REQUIRE(out_dtype == UNUM_DTYPE_BF16 || out_dtype == UNUM_DTYPE_F32,
+               "%s: unsupported out dtype %d", op, out_dtype);
   SaArgs a{};
+  const int st = sa_args(a, op, key_cache, value_cache, kv_row_stride, n_rows, topk_idx,
+                         topk_stride_h, topk_stride_t, topk_stride_k, block_table, bt_stride_b,
+                         slots, token_to_bs, token_pos_in_bs, pos_numel, seqlen_q, seqlen_numel,
+                         T, Hkv, K, B, L);
+  if (st != UNUM_OK) return st;
   a.q = static_cast<const __bf16*>(q);
   a.q_st = q_stride_t;
   a.q_sh = q_stride_h;
-  a.kc = static_cast<const char*>(key_cache);
-  a.vc = static_cast<const char*>(value_cache);
-  a.row_bytes = kv_row_stride * 2;
-  a.n_rows = n_rows;
-  a.idx = topk_idx;
-  a.i_sh = topk_stride_h;
-  a.i_st = topk_stride_t;
-  a.i_sk = topk_stride_k;
-  a.bt = block_table;
-  a.bt_sb = bt_stride_b;
-  a.slots = slots;
-  a.tok_bs = token_to_bs;
-  a.pos = token_pos_in_bs;
-  a.slen = seqlen_q;
-  a.pos_n = static_cast<int32_t>(pos_numel);
-  a.slen_n = static_cast<int32_t>(seqlen_numel == 1 ? 1 : 2);
   a.out = out;
-  a.T = static_cast<int32_t>(T);
-  a.Hkv = static_cast<int32_t>(Hkv);
-  a.K = static_cast<int32_t>(K);
-  a.B = static_cast<int32_t>(B);
-  a.L = static_cast<int32_t>(L);
   a.c = scale * kSaLog2e;
-  UNUM_REQUIRE(out_dtype == UNUM_DTYPE_BF16 || out_dtype == UNUM_DTYPE_F32,
-               "%s: unsupported out dtype %d", op, out_dtype);
   const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(Hkv));
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define UNUM_SA_LAUNCH(OutT, kTab) \
-  hipLaunchKernelGGL((sparse_attn_kernel<OutT, kTab, kSaRing>), grid, dim3(kWave), 0, s, a)
+  hipLaunchKernelGGL((sparse_attn_kernel<OutT, kTab, kSaRing>), grid, dim3(kWave), \
+                     kSaLdsBytes - kSaVBytes, s, a)
   if (out_dtype == UNUM_DTYPE_BF16) {
     if (slots)
       UNUM_SA_LAUNCH(uint16_t, true);
@@ -481,5 +653,37 @@ extern "C" int unum_sparse_paged_attention(
       UNUM_SA_LAUNCH(float, false);
   }
 #undef UNUM_SA_LAUNCH
+  return check_launch(op);
+}
+
+extern "C" int unum_sparse_gather_calibrate(
+    const void* key_cache, const void* value_cache, int64_t kv_row_stride, int64_t n_rows,
+    const int32_t* topk_idx, int64_t topk_stride_h, int64_t topk_stride_t, int64_t topk_stride_k,
+    const int32_t* block_table, int64_t bt_stride_b, const int32_t* slots,
+    const int32_t* token_to_bs, const int32_t* token_pos_in_bs, int64_t pos_numel,
+    const int32_t* seqlen_q, int64_t seqlen_numel, uint32_t* out, int64_t T, int64_t Hkv,
+    int64_t K, int64_t B, int64_t L, void* stream) {
+  using namespace unum;
+  clear_error();
+  const char* op = "sparse_gather_calibrate";
+  UNUM_REQUIRE(T >= 0 && Hkv > 0 && K >= 0 && B >= 0 && L >= 0,
+               "%s: bad sizes (T=%lld Hkv=%lld K=%lld B=%lld L=%lld)", op, (long long)T,
+               (long long)Hkv, (long long)K, (long long)B, (long long)L);
+  if (T == 0) return UNUM_OK;
+  UNUM_REQUIRE(out, "%s: null pointer", op);
+  SaArgs a{};
+  const int st = sa_args(a, op, key_cache, value_cache, kv_row_stride, n_rows, topk_idx,
+                         topk_stride_h, topk_stride_t, topk_stride_k, block_table, bt_stride_b,
+                         slots, token_to_bs, token_pos_in_bs, pos_numel, seqlen_q, seqlen_numel,
+                         T, Hkv, K, B, L);
+  if (st != UNUM_OK) return st;
+  a.out = out;
+  const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(Hkv));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // eight waves per CU, as the attention kernel
+  if (slots)
+    hipLaunchKernelGGL((sparse_gather_kernel<true, kSaRing>), grid, dim3(kWave), kSaLdsBytes, s, a);
+  else
+    hipLaunchKernelGGL((sparse_gather_kernel<false, kSaRing>), grid, dim3(kWave), kSaLdsBytes, s, a);
   return check_launch(op);
 }

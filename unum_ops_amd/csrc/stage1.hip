@@ -89,6 +89,9 @@ __device__ __forceinline__ RowInfo row_info(const Stage1Args& a, int64_t t) {
     vis = tdiv16(lq - 15) + lk - tdiv16(Lq - 16 + 1);
     vis = vis < 0 ? 0 : (vis > lk ? lk : vis);
   }
+  // Keys at or past the output's columns are dropped (in no denominator), as
+  // on every other path.
+  vis = vis < a.out_cols ? vis : static_cast<int32_t>(a.out_cols);
   r.ks = ks;
   r.lk = lk;
   r.vis = vis;
@@ -238,6 +241,14 @@ __device__ __forceinline__ Frag load_q_frag(const Stage1Args& a, int64_t t, int 
   return f;
 }
 
+// Whether key j of a sequence whose first key is row ks of k is read: the
+// rule of every path (the buffer-descriptor paths through readable_keys) --
+// a sequence starting outside [0, Tk) reads no key, and keys at rows past
+// the end of k read none; a key not read scores as a zero key.
+__device__ __forceinline__ bool key_inside(const Stage1Args& a, int64_t ks, int64_t j) {
+  return ks >= 0 && ks < a.Tk && ks + j < a.Tk;
+}
+
 // Score tile: keys [16*jt, 16*jt+16) of the sequence (clamped to stay in the
 // sequence; masked by the caller).  Returns raw q.k (fp32).
 __device__ __forceinline__ f32x4 score_tile(const Stage1Args& a, const Frag& qf,
@@ -245,13 +256,15 @@ __device__ __forceinline__ f32x4 score_tile(const Stage1Args& a, const Frag& qf,
   const int lane = threadIdx.x & (kWave - 1);
   int32_t j = 16 * jt + (lane & 15);
   j = j < ri.lk ? j : ri.lk - 1;
-  int64_t row = ri.ks + j;
-  row = row < a.Tk ? row : a.Tk - 1;  // never read outside k, whatever cu_seqlens_k holds
-  row = row < 0 ? 0 : row;
+  const bool inside = key_inside(a, ri.ks, j);
+  const int64_t row = inside ? ri.ks + j : 0;  // never read outside k, whatever cu_seqlens_k holds
   const __bf16* p = a.k + row * a.k_st + static_cast<int64_t>(g) * a.k_sh + 8 * (lane >> 4);
   bf16x8 kb[kD / 32];
 #pragma unroll
-  for (int c = 0; c < kD / 32; ++c) kb[c] = *reinterpret_cast<const bf16x8*>(p + 32 * c);
+  for (int c = 0; c < kD / 32; ++c) {
+    const i32x4 v = *reinterpret_cast<const i32x4*>(p + 32 * c);
+    kb[c] = __builtin_bit_cast(bf16x8, inside ? v : i32x4{0, 0, 0, 0});
+  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < kD / 32; ++c)
@@ -450,10 +463,8 @@ __global__ __launch_bounds__(64) void stage1_generic_kernel(Stage1Args a) {
   __syncthreads();
   const float c = a.scale_log2;
   auto score = [&](int h, int32_t j) -> float {
-    int64_t row = ri.ks + j;
-    row = row < a.Tk ? row : a.Tk - 1;
-    row = row < 0 ? 0 : row;
-    const __bf16* kp = a.k + row * a.k_st + static_cast<int64_t>(g) * a.k_sh;
+    if (!key_inside(a, ri.ks, j)) return 0.f;  // a key outside k scores as a zero key
+    const __bf16* kp = a.k + (ri.ks + j) * a.k_st + static_cast<int64_t>(g) * a.k_sh;
     float acc = 0.f;
     for (int d = 0; d < D; ++d) acc += qs[h * D + d] * static_cast<float>(kp[d]);
     return acc * c;
@@ -2241,15 +2252,15 @@ extern "C" int unum_infllmv2_attn_stage1(const void* q, int64_t q_stride_t, int6
                              max_seqlen_k, out_cols, scale, causal, "infllmv2_attn_stage1");
   if (st != 0) return st < 0 ? st : UNUM_OK;
   UNUM_REQUIRE(out, "infllmv2_attn_stage1: null output");
+  if (out_dtype != UNUM_DTYPE_F32 && out_dtype != UNUM_DTYPE_BF16)
+    UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "infllmv2_attn_stage1: unsupported out dtype %d", out_dtype);
+  int dev = 0;
+  const int sd = launch_device(stream, "infllmv2_attn_stage1", &dev);
+  if (sd != UNUM_OK) return sd;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (out_dtype) {
-    case UNUM_DTYPE_F32:
-      return launch_stage1<float, false>(a, Stage1Pool{}, workspace, workspace_bytes, s);
-    case UNUM_DTYPE_BF16:
-      return launch_stage1<uint16_t, false>(a, Stage1Pool{}, workspace, workspace_bytes, s);
-    default:
-      UNUM_FAIL(UNUM_ERR_UNSUPPORTED, "infllmv2_attn_stage1: unsupported out dtype %d", out_dtype);
-  }
+  if (out_dtype == UNUM_DTYPE_F32)
+    return launch_stage1<float, false>(a, Stage1Pool{}, workspace, workspace_bytes, s);
+  return launch_stage1<uint16_t, false>(a, Stage1Pool{}, workspace, workspace_bytes, s);
 }
 
 extern "C" int unum_infllmv2_attn_stage1_maxpool(
@@ -2279,6 +2290,9 @@ extern "C" int unum_infllmv2_attn_stage1_maxpool(
   pp.init_blocks = init_blocks;
   pp.local_blocks = local_blocks;
   pp.write_scores = scores != nullptr;
+  int dev = 0;
+  const int sd = launch_device(stream, op, &dev);
+  if (sd != UNUM_OK) return sd;
   return launch_stage1<float, true>(a, pp, workspace, workspace_bytes,
                                     static_cast<hipStream_t>(stream));
 }
@@ -2298,18 +2312,16 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
-// This device's address of `scratch`, or nullptr (with the error set).
-void* scratch_ptr(const char* op) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    set_error("%s: no usable current device (%s)", op,
-              e != hipSuccess ? hipGetErrorString(e) : "device index out of range");
+// Device `dev`'s address of `scratch` (dev is the current device), or
+// nullptr (with the error set).
+void* scratch_ptr(int dev, const char* op) {
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: device index %d out of range", op, dev);
     return nullptr;
   }
   void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
   if (p != nullptr) return p;
-  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || p == nullptr) {
     set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", op, dev,
               hipGetErrorString(e));
@@ -2348,9 +2360,12 @@ extern "C" int unum_infllmv2_attn_stage1_noalloc(
               "%s: this problem splits its keys over %lld bytes of workspace, more than the "
               "%lld-byte device scratch array; call unum_infllmv2_attn_stage1 with a workspace",
               op, (long long)need, (long long)kScratchBytes);
+  int dev = 0;
+  const int sd = launch_device(stream, op, &dev);
+  if (sd != UNUM_OK) return sd;
   void* ws = nullptr;
   if (need > 0) {
-    ws = scratch_ptr(op);
+    ws = scratch_ptr(dev, op);
     if (ws == nullptr) return UNUM_ERR_LAUNCH;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -19,15 +19,29 @@ _OUT_DTYPES = {torch.bfloat16: _lib.UNUM_DTYPE_BF16, torch.float32: _lib.UNUM_DT
 
 def _cache_rows(cache, name, op):
     """(row stride in elements, rows) of a [num_blocks, block_size, Hkv, D]
-    cache viewed as rows of D elements; raises unless that view is uniform."""
+    cache viewed as rows of D elements, row ((n * block_size) + s) * Hkv + h;
+    raises unless those rows are evenly spaced.  Dimensions of size 1 place
+    no constraint, so a one-head slice of a larger cache is accepted."""
     if cache.dim() != 4:
         raise ValueError(f"{op}: {name} must be [num_blocks, block_size, num_kv_heads, head_size]")
     nb, bs, hk, d = cache.shape
     s0, s1, s2, s3 = cache.stride()
-    if s3 != 1 or (bs > 1 and s1 != hk * s2) or (nb > 1 and s0 != bs * s1):
+    row = s2 if hk > 1 else (s1 if bs > 1 else (s0 if nb > 1 else d))
+    if s3 != 1 or (hk > 1 and s2 != row) or (bs > 1 and s1 != hk * row) \
+            or (nb > 1 and s0 != bs * hk * row):
         raise ValueError(f"{op}: {name} rows must be evenly spaced (unit stride in the head "
                          f"dimension, strides {cache.stride()})")
-    return s2, nb * bs * hk
+    return row, nb * bs * hk
+
+
+def _kernel_q(query):
+    """bf16 query with the kernel's layout: unit stride in D, 16-byte aligned
+    base and strides that are multiples of 8 elements (else a packed copy)."""
+    q = query if query.dtype == torch.bfloat16 else query.to(torch.bfloat16)
+    if (q.stride(-1) != 1 or q.data_ptr() % 16 != 0 or q.stride(0) % 8 != 0
+            or q.stride(1) % 8 != 0):
+        q = q.contiguous()
+    return q
 
 
 def sparse_paged_attention(query, key_cache, value_cache, num_heads, num_kv_heads, scale_value,
@@ -65,9 +79,7 @@ def sparse_paged_attention(query, key_cache, value_cache, num_heads, num_kv_head
     if key_cache.shape[2] != Hkv or key_cache.shape[3] != D:
         raise ValueError(f"{op}: caches must be [num_blocks, block_size, {Hkv}, {D}]")
     row_stride, n_rows = _cache_rows(key_cache, "key_cache", op)
-    q = query if query.dtype == torch.bfloat16 else query.to(torch.bfloat16)
-    if q.stride(-1) != 1:
-        q = q.contiguous()
+    q = _kernel_q(query)
     if key_cache.dtype != torch.bfloat16 or value_cache.dtype != torch.bfloat16:
         raise TypeError(f"{op}: the caches must be bfloat16")
     if out is None:
@@ -106,4 +118,44 @@ def sparse_paged_attention(query, key_cache, value_cache, num_heads, num_kv_head
     return out
 
 
-__all__ = ["sparse_paged_attention"]
+def sparse_gather_calibrate(key_cache, value_cache, num_kv_heads, topk_idx, block_table,
+                            token_to_bs, token_pos_in_bs, seqlen_q, slots=None):
+    """Measurement tool, not part of the attention: gathers every K and V row
+    that ``sparse_paged_attention`` with these arguments attends, in its lane
+    pattern and pipeline, with no arithmetic but an XOR checksum.  Returns the
+    u32 checksums ``[T, Hkv, 64]`` (as int32).  Its duration is the floor the
+    gathers alone set for the selection: the roof the attention kernel's time
+    is read against."""
+    op = "sparse_gather_calibrate"
+    dev = require_gpu(op, key_cache, value_cache, topk_idx, block_table, token_to_bs,
+                      token_pos_in_bs, seqlen_q, slots)
+    Hkv, T, K = topk_idx.shape
+    if Hkv != num_kv_heads or key_cache.shape != value_cache.shape \
+            or key_cache.stride() != value_cache.stride() or key_cache.shape[2] != Hkv:
+        raise ValueError(f"{op}: caches must be two [num_blocks, block_size, {Hkv}, D] tensors "
+                         "of one layout")
+    row_stride, n_rows = _cache_rows(key_cache, "key_cache", op)
+    out = torch.empty(T, Hkv, 64, dtype=torch.int32, device=dev)
+    if T == 0:
+        return out
+    idx = topk_idx if topk_idx.dtype == torch.int32 else as_i32(topk_idx, "topk_idx", op)
+    bt = as_i32(block_table, "block_table", op) if (
+        block_table.dtype != torch.int32 or block_table.stride(1) != 1) else block_table
+    B, L = bt.shape
+    bs = as_i32(token_to_bs, "token_to_bs", op).reshape(-1)
+    pos = as_i32(token_pos_in_bs, "token_pos_in_bs", op).reshape(-1)
+    slen = as_i32(seqlen_q, "seqlen_q", op).reshape(-1)
+    sl = None if slots is None else as_i32(slots, "slots", op)
+    lib = _lib.load()
+    with _lib.device_guard(dev):
+        st = lib.unum_sparse_gather_calibrate(
+            _lib.ptr(key_cache), _lib.ptr(value_cache), row_stride, n_rows,
+            _lib.ptr(idx), idx.stride(0), idx.stride(1), idx.stride(2),
+            _lib.ptr(bt), bt.stride(0), _lib.ptr(sl),
+            _lib.ptr(bs), _lib.ptr(pos), pos.numel(), _lib.ptr(slen), slen.numel(),
+            _lib.ptr(out), T, Hkv, K, B, L, _lib.stream_ptr(dev))
+    _lib.check(st, op)
+    return out
+
+
+__all__ = ["sparse_paged_attention", "sparse_gather_calibrate"]
