@@ -19,17 +19,12 @@ from unum_ops_amd import build
 
 SRC = os.path.join(build.HERE, "csrc", "stage1.hip")
 
-# Per-lane scratch allowed for the instances that spill (mangled-name
-# fragment -> bytes); every other instance must use none.  The spills are the
-# eight-quad rows of the LDS-resident kernel (fp32 and bf16 scores) and its
-# largest fused-pool rows: their 168 VGPRs hold the row's 64 exponentials and
-# the redo path's state, and a fourth wave per SIMD would cost more.
-SCRATCH_BUDGET = {
-    "stage1_lds_kernelIfLi8ELb0E": 12,  # fp32 scores, 8 quads
-    "stage1_lds_kernelItLi8ELb0E": 44,  # bf16 scores, 8 quads
-    "stage1_lds_kernelIfLi7ELb1E": 20,  # fused pool, 7 quads
-    "stage1_lds_kernelIfLi8ELb1E": 52,  # fused pool, 8 quads
-}
+# Per-lane scratch allowed for instances that spill (mangled-name fragment ->
+# bytes); every instance not listed must use none.  None is listed: the
+# LDS-resident kernel's eight-quad rows (fp32 and bf16 scores, and with the
+# fused pool) fit their 168 VGPRs -- the row's 64 exponentials included --
+# since each row's queries load at its start instead of a row ahead.
+SCRATCH_BUDGET = {}
 
 
 def _hipcc():

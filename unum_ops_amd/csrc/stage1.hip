@@ -1305,8 +1305,8 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
 // prefill shapes).  One persistent workgroup of twelve waves per CU keeps the
 // whole compressed K of a (sequence, group) in LDS -- 128 KiB in MFMA
 // B-fragment order, filled by buffer-to-LDS loads -- and each wave computes
-// whole (token, group) rows; the next row's queries load into registers
-// while the current row computes.  Every row reads 16 KiB of K fragments
+// whole (token, group) rows, each row's queries loaded at its start (the
+// other waves of the SIMD cover the wait).  Every row reads 16 KiB of K fragments
 // from LDS per 64-key quad, and the LDS delivers more bytes per clock the
 // more waves issue reads: twelve waves (three per SIMD, at most 168 VGPRs)
 // measured faster than eight (which leave room for more registers) and than
@@ -1764,26 +1764,19 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
       row_k_issue<kRowWaves>(a, kt, sg, ntl, wave, sl);
     }
     const bool any = my_row(0) < n;
-    int32_t lq_n = 0;
-    Frag qn;
-    if (any) {
-      lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(0), sg.lq_len));
-      qn = load_q_frag(a, sg.qs + lq_n, sg.g, sl);
-    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // kt is filled
     if (!any) {
       r = sg.end;
       continue;
     }
+    // Each row's queries load at its start.  Loading the next row's a row
+    // ahead (16 registers held through the row) measured the same on cfg3 and
+    // 3 % slower with the fused pool, and pushed the eight-quad instances
+    // into 12-52 B/lane of scratch under the 168-register cap.
     for (int64_t j = 0; my_row(j) < n; ++j) {
-      const Frag qf = qn;
-      const int32_t lq = lq_n;
-      // The next row's queries load into registers while this row computes.
-      if (my_row(j + 1) < n) {
-        lq_n = static_cast<int32_t>(zigzag(sg.k0 + my_row(j + 1), sg.lq_len));
-        qn = load_q_frag(a, sg.qs + lq_n, sg.g, sl);
-      }
+      const int32_t lq = static_cast<int32_t>(zigzag(sg.k0 + my_row(j), sg.lq_len));
+      const Frag qf = load_q_frag(a, sg.qs + lq, sg.g, sl);
       lds_row<OutT, kOutQ, kPool>(a, pp, kl, sg, lq, qf, sel);
     }
     r = sg.end;
