@@ -215,6 +215,33 @@ __device__ __forceinline__ void pool_tail(const Stage1Pool& a, __amdgpu_buffer_r
 
 
 
+// The LDS-resident kernel pools a row's quads into its wave's LDS slot of
+// blocks (lanes 4i of quad qd write block 16qd + i) and stores the row's
+// pooled blocks at the end, each store a run of 64 consecutive blocks (256
+// bytes): the quads' own 64-byte stores, half a 128-byte line each, wrote
+// back about 1.4 times the pooled bytes.  `row` is the wave's slot (LDS
+// writes and reads of one wave complete in order, so no barrier is needed).
+__device__ __forceinline__ void pool_quad_lds(const Stage1Pool& a, float* row, int32_t key0,
+                                              int32_t lk, int32_t ob, float o, float& carry,
+                                              int lane) {
+  const float x = key0 + lane < lk ? o : -INFINITY;
+  float m = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)));
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+  const float left = wave_shr1(x, carry);
+  const int32_t n = (key0 >> 2) + (lane >> 2);
+  const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
+  if ((lane & 3) == 0) row[n] = force ? INFINITY : fmaxf(m, left);
+  carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), kWave - 1));
+}
+
+// Blocks [0, nblk) of the slot to the pooled row (the descriptor's range
+// drops blocks at or past the row's nb).
+__device__ __forceinline__ void pool_flush_lds(__amdgpu_buffer_rsrc_t prs, const float* row,
+                                               int32_t nblk, int lane) {
+  for (int32_t j = lane; j < nblk; j += kWave)
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(row[j]), prs, j * 4, 0, kStoreNT);
+}
+
 // Pooled row of a token outside every sequence: no taps, block of the token 0.
 __device__ __forceinline__ void orphan_pool_row(const Stage1Pool& p, int64_t row,
                                                 int lane = threadIdx.x & (kWave - 1)) {
@@ -1515,6 +1542,7 @@ struct RowPool {
   __amdgpu_buffer_rsrc_t prs;
   int32_t lk;
   int32_t ob;
+  float* slot;  // the wave's LDS slot of pooled blocks (16 * kOutQ floats)
 };
 
 template <typename OutT, int kOutQ, int N, bool kPool>
@@ -1560,7 +1588,8 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
     float carry = -INFINITY;
 #pragma unroll
     for (int qd = 0; qd < kOutQ; ++qd)
-      pool_quad(pp, rp.prs, 64 * qd, rp.lk, rp.ob, ov[qd], carry, false, ln);
+      pool_quad_lds(pp, rp.slot, 64 * qd, rp.lk, rp.ob, ov[qd], carry, ln);
+    pool_flush_lds(rp.prs, rp.slot, 16 * kOutQ, ln);
     pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
   }
 }
@@ -1642,13 +1671,15 @@ __device__ __forceinline__ bool row_fast(KView kl, const Frag& qf, int32_t vis, 
 // the general pipeline against its exact max.
 template <typename OutT, int kOutQ, bool kPool>
 __device__ __forceinline__ void lds_row(const Stage1Args& a, const Stage1Pool& pp, KView kl,
-                                        const Segment& sg, int32_t lq, const Frag& qf, f16x8 sel) {
+                                        const Segment& sg, int32_t lq, const Frag& qf, f16x8 sel,
+                                        float* pslot) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = static_cast<int64_t>(sg.g) * a.Tq + sg.qs + lq;
   OutT* orow = static_cast<OutT*>(a.out) + row * a.out_cols;
   RowPool rp{};
   if constexpr (kPool)
-    rp = RowPool{make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)), sg.lk, lq >> 6};
+    rp = RowPool{make_rsrc(pp.pooled + row * pp.nb, static_cast<uint32_t>(pp.nb * 4)), sg.lk, lq >> 6,
+                 pslot};
   int32_t vis = sg.lk;
   if (a.causal) {
     vis = tdiv16(lq - 15) + sg.lk - tdiv16(sg.lq_len - 16 + 1);
@@ -1668,7 +1699,8 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, const Stage1Pool& p
       float carry = -INFINITY;
 #pragma unroll
       for (int qd = 0; qd < kOutQ; ++qd)
-        pool_quad(pp, rp.prs, 64 * qd, rp.lk, rp.ob, 0.f, carry, false, ln);
+        pool_quad_lds(pp, rp.slot, 64 * qd, rp.lk, rp.ob, 0.f, carry, ln);
+      pool_flush_lds(rp.prs, rp.slot, 16 * kOutQ, ln);
       pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
     }
     return;
@@ -1712,9 +1744,12 @@ template <typename OutT, int kOutQ, bool kPool>
 __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args a, int64_t n_rows,
                                                                        Stage1Pool pp) {
   __shared__ bf16x8 kt[kLdsUnits];                             // 128 KiB
+  // Fused pool: each wave's row of pooled blocks, stored whole (6 KiB).
+  __shared__ float pool_slots[kPool ? kRowWaves * 16 * kOutQ : 1];
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & (kWave - 1);
   const KView kl = make_kview(kt);
+  float* pslot = kPool ? pool_slots + wave * 16 * kOutQ : nullptr;
   // Per-head sum selector (A operand): row m has ones at the k-slots of head
   // m in both tiles, i.e. lane (m, g) at j with 4g + j%4 == m.
   f16x8 sel;
@@ -1777,7 +1812,7 @@ __global__ __launch_bounds__(kRowWaves* kWave) void stage1_lds_kernel(Stage1Args
     for (int64_t j = 0; my_row(j) < n; ++j) {
       const int32_t lq = static_cast<int32_t>(zigzag(sg.k0 + my_row(j), sg.lq_len));
       const Frag qf = load_q_frag(a, sg.qs + lq, sg.g, sl);
-      lds_row<OutT, kOutQ, kPool>(a, pp, kl, sg, lq, qf, sel);
+      lds_row<OutT, kOutQ, kPool>(a, pp, kl, sg, lq, qf, sel, pslot);
     }
     r = sg.end;
   }
