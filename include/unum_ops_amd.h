@@ -133,9 +133,9 @@ int64_t unum_infllmv2_attn_stage1_workspace_size(int64_t B, int64_t Tq, int64_t 
  * targets six workgroups per CU: pieces * splits < 6 * CUs + pieces, with
  * fewer than 6 * CUs pieces whenever keys split, and 1 KiB per (piece,
  * split) plus 48 bytes per piece, so the workspace stays below 12.3 KiB per
- * CU -- 3.14 MiB on a 256-CU MI355X (3.07 MiB is the largest any problem
- * reaches there), and the 4 MiB array holds every problem on GPUs of up to
- * 326 CUs.  Every
+ * CU -- 3.07 MiB on a 256-CU MI355X (2.97 MiB is the largest problem found
+ * there), and the 4 MiB array holds every problem on GPUs of up to 333
+ * CUs.  Every
  * call on one device shares that device's array: calls that overlap on one
  * device (other streams, other threads) race and must be serialised by the
  * caller.  Nothing in the array needs clearing: each call writes every

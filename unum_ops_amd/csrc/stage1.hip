@@ -945,6 +945,18 @@ __device__ __forceinline__ Piece load_piece(const int32_t* src) {
   return pc;
 }
 
+// Key splits: workgroup x of a split's row of workgroups runs piece
+// pair_slot(x) -- pieces 2i and 2i+1 of each run of 16 go to workgroups 8
+// apart, which the dispatcher, dealing workgroups to the 8 XCDs in turn,
+// places on one XCD at about the same time.  With two kv groups every
+// sequence's pieces start at an even index, so the two pieces of a
+// (sequence, group) of 9-16 tokens stream its keys through one L2 instead of
+// two (the grid's row is a multiple of 16, so this is a permutation).
+__device__ __forceinline__ int64_t pair_slot(int64_t x) {
+  const int64_t r = x & 15;
+  return (x - r) + 2 * (r & 7) + (r >> 3);
+}
+
 template <typename OutT, int W, int TW, int CT, int NB, bool kPool, int kSplit>
 __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, Stage1Pool pp,
                                                                  Stage1Split sp) {
@@ -977,14 +989,15 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
   const StreamRead rd = stream_read_offsets();
 
   const int split = kSplit ? static_cast<int>(blockIdx.y) : 0;
+  const int64_t pid = kSplit ? pair_slot(blockIdx.x) : static_cast<int64_t>(blockIdx.x);
   constexpr int kChunkKeys = CT * 16;
   Piece sg;
   if constexpr (kSplit == 2) {
-    sg = load_piece(sp.pieces + static_cast<int64_t>(blockIdx.x) * kPieceInts);
+    sg = load_piece(sp.pieces + pid * kPieceInts);
   } else {
-    sg = find_piece(a, blockIdx.x, R);
+    sg = find_piece(a, pid, R);
     if (kSplit == 1 && split == 0 && threadIdx.x < kWave)
-      store_piece(sp.pieces + static_cast<int64_t>(blockIdx.x) * kPieceInts, sg);
+      store_piece(sp.pieces + pid * kPieceInts, sg);
   }
   if (sg.kind == kOrphan && kSplit != 1 && split == 0) zero_orphan_rows<OutT, kPool>(a, pp, sg, W);
   if (sg.kind == kSeq) {
@@ -1028,7 +1041,7 @@ __global__ __launch_bounds__(W* kWave) void stage1_stream_kernel(Stage1Args a, S
     const bool active = own[0];  // wave-uniform
     auto ws_row = [&](int k) -> int64_t {
       const int64_t i = own[k] ? static_cast<int64_t>(TW) * wave + k : n - 1;
-      return ((static_cast<int64_t>(blockIdx.x) * sp.n_splits) * R + i) * 16;
+      return ((pid * sp.n_splits) * R + i) * 16;
     };
     Frag qf[TW];
 #pragma unroll
@@ -2076,7 +2089,7 @@ SplitPlan split_plan(int64_t Hkv, int64_t Tq, int64_t B, int64_t out_cols) {
   const int R = split_waves(Tq, B) * kStTokensPerWave;
   constexpr int64_t kChunkKeys = kStSplitTiles * 16;
   SplitPlan p{};
-  p.pieces = piece_grid(Hkv, Tq, B, R);
+  p.pieces = (piece_grid(Hkv, Tq, B, R) + 15) / 16 * 16;  // whole runs of 16 for pair_slot
   const int64_t out_chunks = (out_cols + kChunkKeys - 1) / kChunkKeys;
   const int64_t target = 6 * static_cast<int64_t>(num_cus());
   int64_t chunks = (out_chunks * p.pieces + target - 1) / target;
