@@ -239,8 +239,9 @@ int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_numel,
  *            writes it: the topk largest scores, equal scores in ascending
  *            block id, listed in ascending id; -1 for a selected block
  *            scoring -inf and for every slot past num_blocks, -1 entries first.
- * 1 <= num_blocks <= 4096 (when rows > 0), row_stride >= num_blocks,
- * rows < 2^33; NaN scores are outside the contract.
+ * 1 <= num_blocks <= 32768 (when rows > 0), row_stride >= num_blocks,
+ * rows < 2^31 past 4096 blocks (one workgroup per row there) and < 2^33
+ * below; NaN scores are outside the contract.
  */
 int unum_topk_blocks(const float* pooled, int64_t rows, int64_t row_stride, int64_t num_blocks,
                      int32_t* topk_idx, int32_t topk, void* stream);

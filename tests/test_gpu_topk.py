@@ -213,10 +213,53 @@ def test_topk_blocks_bf16_strided_and_wide(dev):
     xb = x.to(torch.bfloat16)
     got = topk_blocks(xb.to(dev), 64)                           # converted to fp32 exactly
     np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(xb.float(), 64))
-    # past 4096 blocks a row: the device sort, same order
+    # past 4096 blocks a row: the workgroup-per-row kernel, same order
     x = _pooled_rows(1, 5, 5000, seed=12, ties=True)
     got = topk_blocks(x.to(dev), 64)
     np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, 64))
+
+
+# Rows past 4096 blocks (contexts past 262 144 tokens): one workgroup per row
+# (256 threads of 32 blocks up to 8192 blocks, then 1024 threads of 16 or
+# 32), every count summed through LDS.  Block counts at and around each
+# size's edge, odd counts (the scalar loads), ties, +-inf blocks.
+@pytest.mark.parametrize("NB", [4097, 5000, 8192, 8193, 16384, 16385, 30001, 32768])
+@pytest.mark.parametrize("topk", [1, 64, 100])
+def test_topk_blocks_wide_rows(NB, topk, dev):
+    x = _pooled_rows(2, 3, NB, seed=NB + topk, ties=NB % 2 == 1)
+    got = topk_blocks(x.to(dev), topk)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
+
+
+def test_topk_blocks_wide_rows_edge_cases(dev):
+    inf = float("inf")
+    NB = 6000
+    g = torch.Generator().manual_seed(5)
+    rows = torch.randn(8, NB, generator=g)
+    rows[0] = 1.0                                   # every score equal: the lowest ids
+    rows[1, 10:] = -inf                             # ten finite blocks, the rest -inf
+    rows[2] = -inf                                  # nothing but -inf
+    rows[3, ::7] = inf                              # more +inf blocks than topk
+    rows[4] = torch.floor(rows[4] * 2.0) / 2.0      # heavy ties at the threshold
+    rows[5, :5000] = -inf                           # a finite tail only
+    rows[6, -3:] = inf                              # +inf at the last thread's blocks
+    x = rows.reshape(1, 8, NB)
+    for topk in (1, 7, 64, 200, 5999, 6000, 6100):  # up to more slots than blocks
+        got = topk_blocks(x.to(dev), topk)
+        np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
+    # rows that are views: bf16, and fp32 at an unaligned offset of a wider buffer
+    wide = torch.zeros(1, 8, NB + 5)
+    wide[..., 1:NB + 1] = x
+    got = topk_blocks(wide.to(dev)[..., 1:NB + 1], 64)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, 64))
+    got = topk_blocks(x.to(torch.bfloat16).to(dev), 64)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x.to(torch.bfloat16).float(), 64))
+
+
+def test_topk_blocks_refuses_rows_past_32768_blocks(dev):
+    with pytest.raises(ValueError, match="exceed"):
+        topk_blocks(torch.zeros(1, 1, 32769, device=dev), 4)
 
 
 def test_topk_blocks_of_fused_stage1_maxpool(dev):

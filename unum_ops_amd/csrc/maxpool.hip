@@ -620,6 +620,129 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* pooled, int
   topk_select<NCH>(key, NB, K, topk + row * K, short_list[threadIdx.x >> 6]);
 }
 
+// Rows of more than 4096 blocks (contexts past 262 144 tokens), past the
+// registers of a wave: one workgroup of kThreads threads per row (256 for up
+// to 8192 blocks, 1024 above), thread j holding blocks j*M .. j*M+M-1 --
+// contiguous, so thread order is block-id order and every rank the output
+// needs is a workgroup prefix sum.  The selection is topk_select's (order
+// (score descending, id ascending), the K-th key built bit by bit, keys
+// equal to it taken by ascending id, -1 first for selected -inf blocks and
+// for slots past NB); each count is summed over the workgroup through LDS.
+constexpr int kTopkLongMaxBlocks = 32 * 1024;  // M <= 32 keys a thread, 1024 threads
+
+// Sum of v over the workgroup's W waves (every thread gets it).  red holds
+// two slots per wave, used alternately: a call's writes cannot overtake the
+// previous call's reads, which every thread finished before that call's
+// barrier.
+template <int W>
+__device__ __forceinline__ int32_t long_sum(int32_t v, int32_t (*red)[W], int& par) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int32_t w = __builtin_amdgcn_readlane(static_cast<int32_t>(wave_incl_sum(static_cast<uint32_t>(v))), kWave - 1);
+  if (lane == 0) red[par][wave] = w;
+  __syncthreads();
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < W; i += 4) {
+    const i32x4 r = *reinterpret_cast<const i32x4*>(&red[par][i]);
+    s += (r.x + r.y) + (r.z + r.w);
+  }
+  par ^= 1;
+  return s;
+}
+
+// Exclusive prefix sum of v over the workgroup's threads in thread order.
+template <int W>
+__device__ __forceinline__ int32_t long_excl_scan(int32_t v, int32_t (*red)[W], int& par) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const int32_t incl = static_cast<int32_t>(wave_incl_sum(static_cast<uint32_t>(v)));
+  if (lane == kWave - 1) red[par][wave] = incl;
+  __syncthreads();
+  int32_t before = 0;
+#pragma unroll
+  for (int i = 0; i < W; ++i) before += i < wave ? red[par][i] : 0;
+  par ^= 1;
+  return before + incl - v;
+}
+
+template <int M, int kThreads, bool kVec>
+__global__ __launch_bounds__(kThreads) void topk_long_kernel(const float* pooled, int64_t row_stride,
+                                                             int32_t NB, int32_t* topk, int32_t K) {
+  constexpr int W = kThreads / kWave;
+  static_assert(W % 4 == 0, "wave counts are summed four at a time");
+  __shared__ __align__(16) int32_t red[2][W];
+  int par = 0;
+  const int64_t row = blockIdx.x;
+  const int j = threadIdx.x;
+  const int32_t n0 = j * M;  // this thread's first block
+  const float* src = pooled + row * row_stride + n0;
+  uint32_t key[M];
+  if (kVec && n0 + M <= NB) {
+#pragma unroll
+    for (int i = 0; i < M; i += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + i);
+      key[i] = order_key(v.x);
+      key[i + 1] = order_key(v.y);
+      key[i + 2] = order_key(v.z);
+      key[i + 3] = order_key(v.w);
+    }
+  } else {
+    // Scalar loads at indices clamped into the row (the last block), so every
+    // load is unconditional; keys past NB are 0, below every real key.
+    const int32_t last = NB - 1 - n0;  // negative for a thread past the row's end
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      const float v = src[i < last ? i : last];
+      key[i] = i <= last ? order_key(v) : 0u;
+    }
+  }
+  auto count = [&](auto pred) -> int32_t {
+    int32_t n = 0;
+#pragma unroll
+    for (int i = 0; i < M; ++i) n += pred(key[i]) ? 1 : 0;
+    return n;
+  };
+  uint32_t tau = 0;     // the K-th largest key (0 when every block is taken)
+  int32_t need_eq = 0;  // blocks with key == tau to take, lowest ids first
+  int32_t neg = 0;      // taken blocks scoring -inf
+  if (NB > K) {
+    // The counts are workgroup-uniform, so every thread takes the same branch.
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = tau | (1u << bit);
+      const int32_t n = long_sum<W>(count([&](uint32_t k) { return k >= cand; }), red, par);
+      if (n >= K) tau = cand;
+      if (n == K) break;
+    }
+    const int32_t gt = tau == 0xffffffffu ? 0 : long_sum<W>(count([&](uint32_t k) { return k > tau; }), red, par);
+    need_eq = K - gt;
+    neg = tau == kKeyNegInf ? need_eq : 0;
+  } else {
+    neg = long_sum<W>(count([&](uint32_t k) { return k == kKeyNegInf; }), red, par);
+  }
+  int32_t lead = (NB < K ? K - NB : 0) + neg;  // -1 slots, first
+  lead = lead < K ? lead : K;
+  int32_t* orow = topk + row * K;
+  for (int32_t i = j; i < lead; i += kThreads) orow[i] = -1;
+  // Keys equal to tau still to take go by ascending id: the thread's rank
+  // among them is the equal keys of the threads before it.
+  const bool rank_eq = need_eq > 0 && tau != kKeyNegInf;
+  int32_t eq_rank = rank_eq ? long_excl_scan<W>(count([&](uint32_t k) { return k == tau; }), red, par) : 0;
+  bool take[M];
+  int32_t n_take = 0;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    const bool eq = key[i] == tau;
+    take[i] = (key[i] > tau || (rank_eq && eq && eq_rank < need_eq)) && key[i] != kKeyNegInf;
+    eq_rank += eq ? 1 : 0;
+    n_take += take[i] ? 1 : 0;
+  }
+  int32_t pos = lead + long_excl_scan<W>(n_take, red, par);
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    if (take[i] && pos < K) orow[pos] = n0 + i;
+    pos += take[i] ? 1 : 0;
+  }
+}
+
 // General path: any P >= 1 (window of P+1 taps, padding 1); one output per lane.
 template <typename T>
 __global__ __launch_bounds__(256) void maxpool_generic_kernel(PoolArgs a) {
@@ -818,16 +941,38 @@ extern "C" int unum_topk_blocks(const float* pooled, int64_t rows, int64_t row_s
                "topk_blocks: bad sizes (rows=%lld, row_stride=%lld, num_blocks=%lld)",
                (long long)rows, (long long)row_stride, (long long)num_blocks);
   UNUM_REQUIRE(topk >= 1, "topk_blocks: topk=%d", topk);
-  UNUM_REQUIRE(num_blocks <= kTopkMaxChunks * 256, "topk_blocks: %lld blocks exceed %d",
-               (long long)num_blocks, kTopkMaxChunks * 256);
+  UNUM_REQUIRE(num_blocks <= kTopkLongMaxBlocks, "topk_blocks: %lld blocks exceed %d",
+               (long long)num_blocks, kTopkLongMaxBlocks);
   if (rows == 0) return UNUM_OK;
   UNUM_REQUIRE(num_blocks >= 1, "topk_blocks: no blocks");
   UNUM_REQUIRE(pooled && topk_idx, "topk_blocks: null pointer");
   const int64_t grid = (rows + 3) / 4;
   UNUM_REQUIRE(grid <= INT32_MAX, "topk_blocks: too many rows (%lld)", (long long)rows);
   const bool vec = (reinterpret_cast<uintptr_t>(pooled) & 15) == 0 && (row_stride % 4) == 0;
-  const int nch = static_cast<int>((num_blocks + 255) / 256);
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (num_blocks > kTopkMaxChunks * 256) {
+    // A workgroup per row: 256 threads of 32 blocks up to 8192 blocks, then
+    // 1024 threads of 16 or 32.
+    UNUM_REQUIRE(rows <= INT32_MAX, "topk_blocks: too many rows (%lld)", (long long)rows);
+    const dim3 gl(static_cast<unsigned>(rows));
+    const int32_t nbl = static_cast<int32_t>(num_blocks);
+#define UNUM_TOPK_LONG(M, TH)                                                                          \
+    if (vec)                                                                                           \
+      hipLaunchKernelGGL((topk_long_kernel<M, TH, true>), gl, dim3(TH), 0, s, pooled, row_stride, nbl, \
+                         topk_idx, topk);                                                              \
+    else                                                                                               \
+      hipLaunchKernelGGL((topk_long_kernel<M, TH, false>), gl, dim3(TH), 0, s, pooled, row_stride, nbl, \
+                         topk_idx, topk)
+    if (num_blocks <= 32 * 256)
+      UNUM_TOPK_LONG(32, 256);
+    else if (num_blocks <= 16 * 1024)
+      UNUM_TOPK_LONG(16, 1024);
+    else
+      UNUM_TOPK_LONG(32, 1024);
+#undef UNUM_TOPK_LONG
+    return check_launch("topk_blocks");
+  }
+  const int nch = static_cast<int>((num_blocks + 255) / 256);
   const dim3 g(static_cast<unsigned>(grid)), b(256);
   const int32_t NB = static_cast<int32_t>(num_blocks);
   switch (nch) {

@@ -44,9 +44,10 @@ def topk_blocks(pooled, topk):
     ``-inf`` are ``-1``; ``topk`` larger than ``NB`` pads with ``-1`` (first).
 
     The selection of ``maxpool_topk`` over scores already pooled (the output of
-    ``infllmv2_attn_stage1_maxpool``): one gfx950 kernel, a row per wave, for
-    up to 4096 blocks a row.  Wider rows (past the kernel's registers) take a
-    stable descending device sort, which orders ties the same way.
+    ``infllmv2_attn_stage1_maxpool``), on gfx950 kernels: a row per wave for up
+    to 4096 blocks a row, a row per workgroup for wider rows (the
+    same selection, its counts summed through LDS), up to 32768 blocks a row
+    (contexts of 2M tokens); wider rows are refused.
     """
     op = "topk_blocks"
     dev = require_gpu(op, pooled)
@@ -56,16 +57,6 @@ def topk_blocks(pooled, topk):
     if topk < 1:
         raise ValueError(f"{op}: topk must be >= 1, got {topk}")
     H, T, NB = pooled.shape
-    if NB > FUSED_MAX_BLOCKS:
-        k = min(topk, NB)
-        vals, idx = torch.sort(pooled, dim=-1, descending=True, stable=True)
-        vals, idx = vals[..., :k], idx[..., :k]
-        idx = torch.where(vals == float("-inf"), torch.full_like(idx, -1), idx)
-        idx = idx.sort(dim=-1).values.to(torch.int32)
-        if k < topk:
-            pad = torch.full((H, T, topk - k), -1, dtype=torch.int32, device=dev)
-            idx = torch.cat([pad, idx], dim=-1)
-        return idx
     x = pooled if pooled.dtype == torch.float32 else pooled.float()  # exact for bf16 / fp16
     if x.stride(-1) != 1 or (T > 1 and x.stride(1) != NB) or (H > 1 and x.stride(0) != T * NB):
         x = x.contiguous()
