@@ -42,6 +42,25 @@ GRAPH_TIMED = ("block_table_cfg5_h16", "block_table_cfg4", "ref_stage1_1024", "r
                "ref_block_table_256")
 
 
+# Untimed back-to-back run of each kernel before its timed launches.  After
+# idle the GPU's clock takes about 25 ms of load to settle: stage 1 on cfg3
+# measured 128-136 us per launch in its first 2 ms and 104-108 us from 25 ms
+# on, batches of 20 launches read by HIP events.
+KERNEL_WARM_S = 0.03
+
+
+def warm(fn, seconds):
+    """Run `fn` back to back for `seconds` of wall time, untimed."""
+    import torch
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 def graph_ms(fn, steps):
     """Milliseconds per call of `fn` as a HIP graph of `steps` captured calls."""
     import torch
@@ -70,7 +89,7 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle timing (e.g. under a profiler)")
     ap.add_argument("--only", choices=["stage1", "maxpool", "block_table", "stage1_cfg5",
@@ -421,11 +440,13 @@ def main():
 
     # Per-kernel launch durations: K back-to-back launches of one kernel
     # between two HIP events on torch's current stream (the stream the
-    # kernels run on), so per-launch event overhead is amortised.
+    # kernels run on), so per-launch event overhead is amortised; each kernel
+    # first runs untimed for KERNEL_WARM_S, so its figure is the settled
+    # clock's.
     per_op = {}
     for name, fn in ops + extra:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        fn()
+        warm(fn, KERNEL_WARM_S)
         e0.record()
         for _ in range(args.steps):
             fn()
