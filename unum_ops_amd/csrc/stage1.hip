@@ -234,6 +234,22 @@ __device__ __forceinline__ void pool_quad_lds(const Stage1Pool& a, float* row, i
   carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), kWave - 1));
 }
 
+// Blocks [first, end) of the slot for quads whose scores are all zero
+// (past the row's visible keys): block n takes its taps from zero columns,
+// present below lk, and the first block its -1 tap from the last computed
+// column, `carry` -- the values pool_quad_lds gives such quads, without their
+// lane moves.
+__device__ __forceinline__ void pool_zero_lds(const Stage1Pool& a, float* row, int32_t first,
+                                              int32_t end, int32_t lk, int32_t ob, float carry,
+                                              int lane) {
+  for (int32_t n = first + lane; n < end; n += kWave) {
+    const bool force = n < a.init_blocks || (ob >= n && ob <= n + a.local_blocks);
+    const bool zero_tap = n == first ? 4 * n < lk : 4 * n - 1 < lk;
+    const float v = fmaxf(n == first ? carry : -INFINITY, zero_tap ? 0.f : -INFINITY);
+    row[n] = force ? INFINITY : v;
+  }
+}
+
 // Blocks [0, nblk) of the slot to the pooled row (the descriptor's range
 // drops blocks at or past the row's nb).
 __device__ __forceinline__ void pool_flush_lds(__amdgpu_buffer_rsrc_t prs, const float* row,
@@ -1601,7 +1617,12 @@ __device__ __forceinline__ void row_store(OutT* orow, const float (&L)[4], const
     float carry = -INFINITY;
 #pragma unroll
     for (int qd = 0; qd < kOutQ; ++qd)
-      pool_quad_lds(pp, rp.slot, 64 * qd, rp.lk, rp.ob, ov[qd], carry, ln);
+      if (qd < N && qd < nq) pool_quad_lds(pp, rp.slot, 64 * qd, rp.lk, rp.ob, ov[qd], carry, ln);
+    // The quads past nq hold zero scores.
+    if (nq < kOutQ) {
+      pool_zero_lds(pp, rp.slot, 16 * nq, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
+      carry = 64 * kOutQ - 1 < rp.lk ? 0.f : -INFINITY;
+    }
     pool_flush_lds(rp.prs, rp.slot, 16 * kOutQ, ln);
     pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
   }
@@ -1709,12 +1730,9 @@ __device__ __forceinline__ void lds_row(const Stage1Args& a, const Stage1Pool& p
     if constexpr (kPool) {
       int ln = lane;  // opaque: see row_store
       asm volatile("" : "+v"(ln));
-      float carry = -INFINITY;
-#pragma unroll
-      for (int qd = 0; qd < kOutQ; ++qd)
-        pool_quad_lds(pp, rp.slot, 64 * qd, rp.lk, rp.ob, 0.f, carry, ln);
+      pool_zero_lds(pp, rp.slot, 0, 16 * kOutQ, rp.lk, rp.ob, -INFINITY, ln);
       pool_flush_lds(rp.prs, rp.slot, 16 * kOutQ, ln);
-      pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, carry, ln);
+      pool_tail(pp, rp.prs, 16 * kOutQ, rp.lk, rp.ob, 64 * kOutQ - 1 < rp.lk ? 0.f : -INFINITY, ln);
     }
     return;
   }
