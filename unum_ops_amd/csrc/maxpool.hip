@@ -650,6 +650,28 @@ __device__ __forceinline__ int32_t long_sum(int32_t v, int32_t (*red)[W], int& p
   return s;
 }
 
+// Largest and smallest of v over the workgroup (every thread gets both);
+// the same two-slot scheme as long_sum.
+template <int W>
+__device__ __forceinline__ void long_max_min(uint32_t vmax, uint32_t vmin, uint32_t (*red)[2 * W],
+                                             int& par, uint32_t& hi, uint32_t& lo) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const uint32_t a = wave_max_u32(vmax), b = wave_min_u32(vmin);
+  if (lane == 0) {
+    red[par][wave] = a;
+    red[par][W + wave] = b;
+  }
+  __syncthreads();
+  hi = 0u;
+  lo = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    hi = max(hi, red[par][i]);
+    lo = min(lo, red[par][W + i]);
+  }
+  par ^= 1;
+}
+
 // Exclusive prefix sum of v over the workgroup's threads in thread order.
 template <int W>
 __device__ __forceinline__ int32_t long_excl_scan(int32_t v, int32_t (*red)[W], int& par) {
@@ -670,7 +692,8 @@ __global__ __launch_bounds__(kThreads) void topk_long_kernel(const float* pooled
   constexpr int W = kThreads / kWave;
   static_assert(W % 4 == 0, "wave counts are summed four at a time");
   __shared__ __align__(16) int32_t red[2][W];
-  int par = 0;
+  __shared__ uint32_t red_mm[2][2 * W];
+  int par = 0, par_mm = 0;
   const int64_t row = blockIdx.x;
   const int j = threadIdx.x;
   const int32_t n0 = j * M;  // this thread's first block
@@ -705,8 +728,28 @@ __global__ __launch_bounds__(kThreads) void topk_long_kernel(const float* pooled
   int32_t need_eq = 0;  // blocks with key == tau to take, lowest ids first
   int32_t neg = 0;      // taken blocks scoring -inf
   if (NB > K) {
-    // The counts are workgroup-uniform, so every thread takes the same branch.
-    for (int bit = 31; bit >= 0; --bit) {
+    // The counts are workgroup-uniform, so every thread takes the same
+    // branch.  Bounds on tau fix its high bits, as in topk_select: while
+    // fewer than K blocks are +inf, tau is at most the largest finite key,
+    // and when at least K threads hold blocks, at least the smallest of
+    // their largest keys (distinct keys, one a thread).
+    int top = 31;
+    const int32_t holders = (NB + M - 1) / M;  // threads holding a block
+    if (K <= holders && long_sum<W>(count([&](uint32_t k) { return k >= kKeyPosInf; }), red, par) < K) {
+      uint32_t tmax = 0;
+#pragma unroll
+      for (int i = 0; i < M; ++i) tmax = max(tmax, key[i] < kKeyPosInf ? key[i] : 0u);
+      uint32_t hi, lo;
+      long_max_min<W>(tmax, n0 < NB ? tmax : 0xffffffffu, red_mm, par_mm, hi, lo);
+      if (lo == hi) {
+        top = -1;  // tau == hi
+        tau = hi;
+      } else {
+        top = 31 - __builtin_clz(lo ^ hi);
+        tau = hi & ~((2u << top) - 1u);  // the shared bits above `top`
+      }
+    }
+    for (int bit = top; bit >= 0; --bit) {
       const uint32_t cand = tau | (1u << bit);
       const int32_t n = long_sum<W>(count([&](uint32_t k) { return k >= cand; }), red, par);
       if (n >= K) tau = cand;
