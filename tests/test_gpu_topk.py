@@ -83,10 +83,11 @@ def test_most_keys_between_the_bounds(dev):
 
 
 def _list_rows(T, ties, seed):
-    """2112-block rows (nine chunks a lane) for the search over the short list:
-    lane 0's largest key, 0.1, is the lower bound; every other lane holds an
-    anchor in [0.12, 0.18]; everything else is below 0.05 but for m_r large
-    keys outside lane 0, so row r's list holds 64 + m_r keys."""
+    """2112-block rows (nine chunks a lane) for the selection over the list:
+    lane 0's largest score, 0.1, is the lower bound; every other lane holds an
+    anchor in [0.12, 0.18] (lane 63 also a +inf block); everything else is
+    below 0.05 but for m_r large scores outside lane 0, so row r's list holds
+    65 + m_r entries."""
     g = torch.Generator().manual_seed(seed)
     x = torch.rand(1, T, 2112, generator=g) * 0.05
     anchor = 4 * torch.arange(64)                   # block 4l: lane l, chunk 0
@@ -104,14 +105,14 @@ def _list_rows(T, ties, seed):
             v = torch.floor(v * 64.0) / 64.0
         x[0, r, cols] = v
         ms.append(m)
-    x[0, :, 1] = float("inf")
+    x[0, :, 4 * 63 + 1] = float("inf")
     return x, ms
 
 
 @pytest.mark.parametrize("ties", [False, True])
 def test_short_list_of_every_length(ties, dev):
-    # Lists of 64 to 1024 keys (one to sixteen a lane) and, on the last rows,
-    # more than 1024 (the search then counts every key).
+    # Lists of 65 to 1565 entries: one to ten a lane, and past 640 (the row
+    # then runs topk_select, whose own short list takes up to 1024 keys).
     x, _ = _list_rows(40, ties, 31 + ties)
     for topk in (1, 64):
         got = topk_blocks(x.to(dev), topk)
@@ -202,6 +203,62 @@ def test_topk_blocks_small_cases(dev):
     ties = torch.tensor([[[1.0, 2.0, 2.0, 2.0, 0.5, 2.0]]]).to(dev)
     assert topk_blocks(ties, 2).cpu().tolist() == [[[1, 2]]]
     assert topk_blocks(ties, 4).cpu().tolist() == [[[1, 2, 3, 5]]]
+
+
+def _list_case_rows(kind, T, NB, g):
+    """Rows of two chunks or more for the list selection (topk <= 64) and the
+    cases it hands to topk_select."""
+    inf = float("inf")
+    u = torch.rand(T, NB, generator=g)
+    if kind == "uniform":
+        return u
+    if kind == "negative":            # no score >= 0: each lane's largest is its least negative
+        return -u - 1.0
+    if kind == "signed_zeros":        # -0.0 and +0.0 are one score: ties by ascending id
+        x = torch.where(torch.rand(T, NB, generator=g) < 0.5, torch.tensor(-0.0), torch.tensor(0.0))
+        x[:, torch.randperm(NB, generator=g)[:20]] = 1.0
+        x[:, torch.randperm(NB, generator=g)[:NB // 2]] = -1.0
+        return x
+    if kind == "many_inf":            # more +inf blocks than slots
+        x = u.clone()
+        x[:, torch.randperm(NB, generator=g)[:100]] = inf
+        return x
+    if kind == "mostly_minus_inf":    # fewer finite blocks than slots: -inf selected (-1)
+        x = torch.full((T, NB), -inf)
+        x[:, torch.randperm(NB, generator=g)[:30]] = u[:, :30]
+        return x
+    if kind == "wide_tie":            # 64 + tied blocks at the cut, every lane holding one
+        x = u * 0.1
+        x[:, 0:256:4] = 0.5
+        x[:, torch.randperm(NB, generator=g)[:40]] = 0.5
+        x[:, torch.randperm(NB, generator=g)[:10]] = 0.9
+        return x
+    if kind == "coarse":              # few distinct scores: ties and long lists
+        return torch.floor(u * 6.0)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["uniform", "negative", "signed_zeros", "many_inf",
+                                  "mostly_minus_inf", "wide_tie", "coarse"])
+@pytest.mark.parametrize("NB", [257, 600, 2112, 4096])
+def test_topk_blocks_list_selection(kind, NB, dev):
+    g = torch.Generator().manual_seed(NB * 13 + len(kind))
+    x = _list_case_rows(kind, 12, NB, g).reshape(1, 12, NB)
+    for topk in (1, 7, 64, 65):       # 65: past the list selection
+        got = topk_blocks(x.to(dev), topk)
+        np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
+
+
+@pytest.mark.parametrize("NB", [200, 2112, 5000])
+def test_topk_blocks_signed_zeros(NB, dev):
+    # One chunk, the list selection, and one workgroup a row: -0.0 ranks as
+    # +0.0 everywhere (the oracle's argsort compares them equal).
+    x = torch.zeros(2, 5, NB)
+    x[:, :, 1::3] = -0.0
+    x[:, :, 7] = 2.0
+    x[1, :, ::5] = -1.0
+    got = topk_blocks(x.to(dev), 64)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, 64))
 
 
 def test_topk_blocks_bf16_strided_and_wide(dev):

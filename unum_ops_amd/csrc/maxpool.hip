@@ -298,15 +298,26 @@ constexpr int kTopkMaxChunks = 16;  // NB <= 4096 (64 keys per lane)
 constexpr uint32_t kKeyNegInf = 0x007fffffu;  // order_key(-inf)
 constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)
 constexpr int kTopkShortList = 1024;  // keys between the bounds kept per wave (16 a lane)
+constexpr int kTopkListCap = 640;     // (score, id) pairs of topk_select_list's wave list
 
-// Storage of the per-wave short lists of a 256-thread block: none with one
-// chunk a row, where the search counts the keys in registers.
+// LDS words of each wave of a 256-thread block: topk_select_list's list of
+// score bits and block ids (reused afterwards for its bitmaps), which also
+// holds topk_select's short list; none with one chunk a row, where the search
+// counts the keys in registers.
 template <int NCH>
-constexpr int topk_list_len() { return NCH >= 2 ? kTopkShortList : 1; }
+constexpr int topk_list_len() { return NCH >= 2 ? 2 * kTopkListCap : 1; }
+static_assert(2 * kTopkListCap >= kTopkShortList, "the short list shares the wave's LDS");
 
+// Order-preserving unsigned key of a score; -0.0 maps to +0.0's key, since
+// the two are equal scores (ties, taken in ascending block id).
 __device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t b = __float_as_uint(f);
+  uint32_t b = __float_as_uint(f);
+  b = b == 0x80000000u ? 0u : b;
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+// The score of a key order_key returns.
+__device__ __forceinline__ float key_score(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 // Wave-wide max / min (wave-uniform results): DPP within each 16-lane row
@@ -567,6 +578,213 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
   }
 }
 
+// ----------------------------------------- list selection (two chunks or more)
+// For rows of two or more chunks and K <= 64, the selection of topk_select
+// over a list instead of the 4*NCH keys a lane.  The K-th largest score is at
+// least lo, the smallest of the lanes' largest scores (64 scores lie at or
+// above it), so every score >= lo goes, with its block id, to a per-wave list
+// in LDS (cfg5's real pooled rows: 202-704 of 2112 blocks, measured on the CPU
+// from the oracle's rows), and the threshold search, the tie rule and the
+// output run over its entries alone -- ceil(total/64) a lane.  The output
+// needs no sort: the taken blocks are marked in a bitmap of the row (64
+// blocks a lane), and an entry's slot is the number of taken blocks below it.
+// Equal scores still to rank (fewer taken than tied) are ranked the same way
+// through a bitmap of the tied blocks.  Scores past NB are -inf here: they
+// rank after every real -inf block (higher ids), so they are taken only where
+// a real -inf block would be too, and a taken -inf block is written as -1
+// whatever its id.
+
+// Bits of the 64-bit word (lo, hi) below bit b.
+__device__ __forceinline__ int32_t bits_below(uint32_t lo, uint32_t hi, int b) {
+  const uint64_t w = (static_cast<uint64_t>(hi) << 32) | lo;
+  return __popcll(w & ((uint64_t(1) << b) - 1u));
+}
+__device__ __forceinline__ void lds_or(uint32_t* p, uint32_t bit) {
+  __hip_atomic_fetch_or(p, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
+// The list holds `total` entries, entry i's score bits at lds[i] and block id
+// at lds[kTopkListCap + i]; NS = ceil(total / 64).  lo is the key of the smallest lane
+// maximum: every key of the row >= lo is in the list.
+template <int NS>
+__device__ __forceinline__ void list_select(uint32_t* lds, int32_t total, uint32_t lo, int32_t K,
+                                            int32_t* orow) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t sk[NS];
+  int32_t sid[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int idx = i * kWave + lane;  // < NS*64 <= kTopkListCap: inside the list
+    const uint32_t b = lds[idx], id = lds[kTopkListCap + idx];
+    sk[i] = idx < total ? order_key(__uint_as_float(b)) : 0u;  // key 0: below every candidate
+    sid[i] = idx < total ? static_cast<int32_t>(id) : 0;
+  }
+  auto count = [&](auto pred) -> int32_t {
+    int32_t n = 0;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) n += __popcll(__ballot(pred(sk[i])));
+    return n;
+  };
+  // tau: the K-th largest key.  With K or more +inf scores it is +inf;
+  // otherwise lo is a finite list key, hi (the largest finite one) >= lo, and
+  // tau in [lo, hi] shares every bit above the highest bit where they differ.
+  uint32_t tau = kKeyPosInf;
+  int top = -1;
+  if (count([](uint32_t k) { return k == kKeyPosInf; }) < K) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) m = (sk[i] < kKeyPosInf && sk[i] > m) ? sk[i] : m;
+    const uint32_t hi = wave_max_u32(m);
+    if (hi == lo) {
+      tau = lo;
+    } else {
+      top = 31 - __builtin_clz(lo ^ hi);
+      tau = hi & ~((2u << top) - 1u);
+    }
+  }
+  // Below lo the list undercounts but still holds >= 64 >= K keys, so the
+  // `>= K` decisions stand; the exact-K stop waits for a candidate past lo.
+  for (int bit = top; bit >= 0; --bit) {
+    const uint32_t cand = tau | (1u << bit);
+    const int32_t n = count([cand](uint32_t k) { return k >= cand; });
+    if (n >= K) tau = cand;
+    if (n == K && cand > lo) break;
+  }
+  const int32_t need_eq = K - count([tau](uint32_t k) { return k > tau; });  // >= 0
+  const bool neg = tau == kKeyNegInf;  // the tied blocks score -inf: -1 slots, first
+  const int32_t n_eq = need_eq > 0 && !neg ? count([tau](uint32_t k) { return k == tau; }) : 0;
+  const bool rank_eq = need_eq > 0 && need_eq < n_eq;
+  bool take[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+    take[i] = sk[i] > tau || (sk[i] == tau && need_eq > 0 && !neg && !rank_eq);
+
+  // The list has been read into registers: its LDS now holds the bitmaps.
+  uint32_t* bm = lds;          // taken blocks: bit n % 32 of word n / 32
+  uint32_t* before = lds + 128;  // taken blocks below lane l's 64 blocks
+  __builtin_amdgcn_wave_barrier();
+  bm[2 * lane] = 0u;
+  bm[2 * lane + 1] = 0u;
+  if (rank_eq) {
+    uint32_t* em = lds + 192;   // tied blocks
+    uint32_t* eb = lds + 320;   // tied blocks below lane l's 64 blocks
+    em[2 * lane] = 0u;
+    em[2 * lane + 1] = 0u;
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+      if (sk[i] == tau) lds_or(em + (sid[i] >> 5), 1u << (sid[i] & 31));
+    __builtin_amdgcn_wave_barrier();
+    const int32_t c = __popc(em[2 * lane]) + __popc(em[2 * lane + 1]);
+    eb[lane] = wave_incl_sum(c) - c;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      if (sk[i] == tau) {
+        const int L = sid[i] >> 6;
+        take[i] = static_cast<int32_t>(eb[L]) + bits_below(em[2 * L], em[2 * L + 1], sid[i] & 63) < need_eq;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+    if (take[i]) lds_or(bm + (sid[i] >> 5), 1u << (sid[i] & 31));
+  __builtin_amdgcn_wave_barrier();
+  const int32_t c = __popc(bm[2 * lane]) + __popc(bm[2 * lane + 1]);
+  before[lane] = wave_incl_sum(c) - c;
+  __builtin_amdgcn_wave_barrier();
+  const int32_t lead = neg ? need_eq : 0;
+  if (lane < lead) orow[lane] = -1;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    if (take[i]) {
+      const int L = sid[i] >> 6;
+      // lead + the taken blocks is K; the bound only keeps NaN scores (outside
+      // the contract) inside the row.
+      const int32_t slot = lead + static_cast<int32_t>(before[L]) + bits_below(bm[2 * L], bm[2 * L + 1], sid[i] & 63);
+      if (slot < K) orow[slot] = sid[i];
+    }
+  }
+}
+
+// Builds the list from the lane's scores v (block 256*ch + 4*lane + e; -inf
+// past NB) and selects from it; false, with nothing written, when more than
+// kTopkListCap scores are >= lo.
+template <int NCH>
+__device__ __forceinline__ bool topk_select_list(const float (&v)[NCH][4], int32_t K, int32_t* orow,
+                                                 uint32_t* lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  // The lane's largest score from the scores' bits as integers: the largest
+  // of them when a score has the sign bit clear, else the smallest (sign and
+  // magnitude order negative scores the other way round).
+  int32_t imax = INT32_MIN, imin = INT32_MAX;
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int32_t b = __float_as_int(v[ch][e]);
+      imax = b > imax ? b : imax;
+      imin = b < imin ? b : imin;
+    }
+  const uint32_t lo = wave_min_u32(order_key(__int_as_float(imax >= 0 ? imax : imin)));
+  const float lo_score = key_score(lo);
+  // Scores >= lo go to the list slot by slot ((ch, e) in turn, lanes in
+  // order within a slot); a chunk that would pass the cap ends the attempt.
+  uint32_t total = 0;  // wave-uniform
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    bool in[4];
+    uint64_t m[4];
+    uint32_t n = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      in[e] = v[ch][e] >= lo_score;
+      m[e] = __ballot(in[e]);
+      n += static_cast<uint32_t>(__popcll(m[e]));
+    }
+    if (total + n > kTopkListCap) return false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (in[e]) {
+        const uint32_t pos = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m[e] >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m[e]), total));
+        lds[pos] = __float_as_uint(v[ch][e]);
+        lds[kTopkListCap + pos] = static_cast<uint32_t>(256 * ch + 4 * lane + e);
+      }
+      total += static_cast<uint32_t>(__popcll(m[e]));
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  switch ((total + kWave - 1) / kWave) {
+#define TOPK_LIST(N) \
+  case N: list_select<N>(lds, static_cast<int32_t>(total), lo, K, orow); return true;
+    TOPK_LIST(1) TOPK_LIST(2) TOPK_LIST(3) TOPK_LIST(4) TOPK_LIST(5)
+    TOPK_LIST(6) TOPK_LIST(7) TOPK_LIST(8) TOPK_LIST(9) TOPK_LIST(10)
+#undef TOPK_LIST
+    default: return false;  // no score >= lo: NaN scores
+  }
+}
+static_assert(kTopkListCap == 10 * kWave, "list_select is instantiated for 1..10 entries a lane");
+
+// The selection of a row whose lane holds scores v (block 256*ch + 4*lane +
+// e, -inf past NB): the list selection when it applies, else topk_select.
+// topk_select takes the -inf past NB as blocks of the row (NCH*256 of them):
+// they rank after every real block, so they are taken only where a real -inf
+// block would be, and -- -inf -- are written as -1 like those; the -1 count
+// K - NB of slots past a short row comes out the same.
+template <int NCH>
+__device__ __forceinline__ void select_row(const float (&v)[NCH][4], int32_t K, int32_t* orow,
+                                           uint32_t* lds) {
+  if constexpr (NCH >= 2) {
+    if (K <= kWave && topk_select_list<NCH>(v, K, orow, lds)) return;
+  }
+  uint32_t key[NCH][4];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) key[ch][e] = order_key(v[ch][e]);
+  topk_select<NCH>(key, 256 * NCH, K, orow, lds);
+}
+
 template <int NCH>
 __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* topk, int32_t K,
                                                            int32_t store) {
@@ -576,17 +794,17 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   const int lane = threadIdx.x & (kWave - 1);
   const RowCtx c = row_ctx(a, row, t);
   const int32_t NB = static_cast<int32_t>(a.NB);
-  __shared__ uint32_t short_list[4][topk_list_len<NCH>()];  // one per wave of the 256-thread block
-  uint32_t key[NCH][4];
+  __shared__ uint32_t lds[4][topk_list_len<NCH>()];  // one per wave of the 256-thread block
+  float v[NCH][4];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     float r[4];
     pool4<float, true>(a, c, ch, r);
     if (store) store_pooled<float, true>(a, row, ch * 256 + 4 * lane, r);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) key[ch][e] = (256 * ch + 4 * lane + e < NB) ? order_key(r[e]) : 0u;
+    for (int e = 0; e < 4; ++e) v[ch][e] = 256 * ch + 4 * lane + e < NB ? r[e] : -INFINITY;
   }
-  topk_select<NCH>(key, NB, K, topk + row * K, short_list[threadIdx.x >> 6]);
+  select_row<NCH>(v, K, topk + row * K, lds[threadIdx.x >> 6]);
 }
 
 // The same selection over rows already pooled (the fused stage-1 + max-pool
@@ -597,27 +815,38 @@ template <int NCH, bool kVec>
 __global__ __launch_bounds__(256) void topk_rows_kernel(const float* pooled, int64_t rows,
                                                         int64_t row_stride, int32_t NB,
                                                         int32_t* topk, int32_t K) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + (threadIdx.x / kWave);
-  if (row >= rows) return;  // wave-uniform
+  // The wave's row, wave-uniform for the compiler (readfirstlane): the
+  // branches on per-row values below are scalar branches.
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (row >= rows) return;
   const int lane = threadIdx.x & (kWave - 1);
   const float* src = pooled + row * row_stride;
-  __shared__ uint32_t short_list[4][topk_list_len<NCH>()];
-  uint32_t key[NCH][4];
+  __shared__ uint32_t lds[4][topk_list_len<NCH>()];
+  // Every chunk's loads are issued before any is used: buffer loads of the
+  // row (its NB scores: past them the range check reads 0), the lane's offset
+  // in one register and the chunk's in the instruction, a chunk inside the
+  // row as one 16-byte load and the row's last chunk score by score (a
+  // wave-uniform branch).  Per-lane branches between two load forms of the
+  // same registers made the compiler wait for every earlier load before each
+  // chunk's.
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, static_cast<uint32_t>(NB) * 4u);
+  float v[NCH][4];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     const int32_t n0 = 256 * ch + 4 * lane;
-    float r[4];
-    if (kVec && n0 + 3 < NB) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(src + n0);
-      r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+    if (kVec && 256 * ch + 256 <= NB) {
+      const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, 1024 * ch, 0));
+      v[ch][0] = x.x; v[ch][1] = x.y; v[ch][2] = x.z; v[ch][3] = x.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = n0 + e < NB ? src[n0 + e] : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        const float x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (n0 + e), 0, 0));
+        v[ch][e] = n0 + e < NB ? x : -INFINITY;
+      }
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) key[ch][e] = n0 + e < NB ? order_key(r[e]) : 0u;
   }
-  topk_select<NCH>(key, NB, K, topk + row * K, short_list[threadIdx.x >> 6]);
+  select_row<NCH>(v, K, topk + row * K, lds[threadIdx.x >> 6]);
 }
 
 // Rows of more than 4096 blocks (contexts past 262 144 tokens), past the
