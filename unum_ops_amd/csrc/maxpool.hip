@@ -796,13 +796,54 @@ __global__ __launch_bounds__(256) void maxpool_topk_kernel(PoolArgs a, int32_t* 
   const int32_t NB = static_cast<int32_t>(a.NB);
   __shared__ uint32_t lds[4][topk_list_len<NCH>()];  // one per wave of the 256-thread block
   float v[NCH][4];
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) {
+  if constexpr (NCH == 1) {
     float r[4];
-    pool4<float, true>(a, c, ch, r);
-    if (store) store_pooled<float, true>(a, row, ch * 256 + 4 * lane, r);
+    pool4<float, true>(a, c, 0, r);
+    if (store) store_pooled<float, true>(a, row, 4 * lane, r);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[ch][e] = 256 * ch + 4 * lane + e < NB ? r[e] : -INFINITY;
+    for (int e = 0; e < 4; ++e) v[0][e] = 4 * lane + e < NB ? r[e] : -INFINITY;
+  } else {
+    // Rows of several chunks: chunk ch+1's taps are loaded while chunk ch is
+    // pooled (two tap buffers), so a row's loads overlap instead of waiting
+    // chunk by chunk.  Every chunk is four 16-byte buffer loads a lane over
+    // the row's taps below lim: the range check is per 4-byte word, so the
+    // words past lim read 0 (masked to -inf by pool_taps) and no branch
+    // separates the loads.  Lane 0's tap 4*n0-1 is the previous chunk's last
+    // tap, from lane 63.
+    // The row's start and limit are wave-uniform: readfirstlane lets the
+    // compiler keep the resource in scalar registers.
+    const uint64_t row_addr = reinterpret_cast<uint64_t>(static_cast<const float*>(a.in) + c.base);
+    const uint64_t ra = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(row_addr >> 32))) << 32) |
+                        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(row_addr)));
+    const int32_t lim = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(c.lim));  // <= 4*NB
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(reinterpret_cast<const float*>(ra), static_cast<uint32_t>(lim) * 4u);
+    float tb[2][16];
+    auto issue = [&](int ch, float (&d)[16]) {
+      const int off = 4 * (1024 * ch + 16 * lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * j, 0, 0));
+        d[4 * j] = x.x; d[4 * j + 1] = x.y; d[4 * j + 2] = x.z; d[4 * j + 3] = x.w;
+      }
+    };
+    issue(0, tb[0]);
+    float carry = -INFINITY;  // tap 1024*ch - 1, for lane 0
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      if (ch + 1 < NCH) issue(ch + 1, tb[(ch + 1) & 1]);
+      Taps tp;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) tp.v[j] = tb[ch & 1][j];
+      tp.below = carry;
+      float r[4];
+      pool_taps(a, c, ch, tp, r);
+      carry = 1024 * ch + 1023 < lim
+                  ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tp.v[15]), 63))
+                  : -INFINITY;
+      if (store) store_pooled<float, true>(a, row, ch * 256 + 4 * lane, r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[ch][e] = 256 * ch + 4 * lane + e < NB ? r[e] : -INFINITY;
+    }
   }
   select_row<NCH>(v, K, topk + row * K, lds[threadIdx.x >> 6]);
 }
@@ -823,28 +864,25 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* pooled, int
   const int lane = threadIdx.x & (kWave - 1);
   const float* src = pooled + row * row_stride;
   __shared__ uint32_t lds[4][topk_list_len<NCH>()];
-  // Every chunk's loads are issued before any is used: buffer loads of the
-  // row (its NB scores: past them the range check reads 0), the lane's offset
-  // in one register and the chunk's in the instruction, a chunk inside the
-  // row as one 16-byte load and the row's last chunk score by score (a
-  // wave-uniform branch).  Per-lane branches between two load forms of the
-  // same registers made the compiler wait for every earlier load before each
-  // chunk's.
+  // Every chunk's loads are issued before any is used: one 16-byte buffer
+  // load a lane and chunk over the row's NB scores (four 4-byte loads for
+  // rows not 16-byte aligned), with no branch between them: the range check
+  // is per 4-byte word, so the words past NB read 0 (replaced by -inf).
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, static_cast<uint32_t>(NB) * 4u);
   float v[NCH][4];
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     const int32_t n0 = 256 * ch + 4 * lane;
-    if (kVec && 256 * ch + 256 <= NB) {
-      const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, 1024 * ch, 0));
+    if constexpr (kVec) {  // 16-byte aligned rows
+      const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 4 * n0, 0, 0));
       v[ch][0] = x.x; v[ch][1] = x.y; v[ch][2] = x.z; v[ch][3] = x.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (n0 + e), 0, 0));
-        v[ch][e] = n0 + e < NB ? x : -INFINITY;
-      }
+      for (int e = 0; e < 4; ++e)
+        v[ch][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, 4 * (n0 + e), 0, 0));
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[ch][e] = n0 + e < NB ? v[ch][e] : -INFINITY;
   }
   select_row<NCH>(v, K, topk + row * K, lds[threadIdx.x >> 6]);
 }
