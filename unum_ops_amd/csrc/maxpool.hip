@@ -584,8 +584,10 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
 // least lo, the smallest of the lanes' largest scores (64 scores lie at or
 // above it), so every score >= lo goes, with its block id, to a per-wave list
 // in LDS (cfg5's real pooled rows: 202-704 of 2112 blocks, measured on the CPU
-// from the oracle's rows), and the threshold search, the tie rule and the
-// output run over its entries alone -- ceil(total/64) a lane.  The output
+// from the oracle's rows; past kTopkListCap, lo is first raised by steps of
+// the threshold search over the lane's scores), and the threshold search, the
+// tie rule and the output run over its entries alone -- ceil(total/64) a
+// lane.  The output
 // needs no sort: the taken blocks are marked in a bitmap of the row (64
 // blocks a lane), and an entry's slot is the number of taken blocks below it.
 // Equal scores still to rank (fewer taken than tied) are ranked the same way
@@ -604,8 +606,8 @@ __device__ __forceinline__ void lds_or(uint32_t* p, uint32_t bit) {
 }
 
 // The list holds `total` entries, entry i's score bits at lds[i] and block id
-// at lds[kTopkListCap + i]; NS = ceil(total / 64).  lo is the key of the smallest lane
-// maximum: every key of the row >= lo is in the list.
+// at lds[kTopkListCap + i]; NS = ceil(total / 64).  Every key of the row >= lo
+// is in the list, and at least K keys are.
 template <int NS>
 __device__ __forceinline__ void list_select(uint32_t* lds, int32_t total, uint32_t lo, int32_t K,
                                             int32_t* orow) {
@@ -626,8 +628,9 @@ __device__ __forceinline__ void list_select(uint32_t* lds, int32_t total, uint32
     return n;
   };
   // tau: the K-th largest key.  With K or more +inf scores it is +inf;
-  // otherwise lo is a finite list key, hi (the largest finite one) >= lo, and
-  // tau in [lo, hi] shares every bit above the highest bit where they differ.
+  // otherwise the list holds a finite key >= lo, hi (the largest one) >= lo,
+  // and tau in [lo, hi] shares every bit above the highest bit where they
+  // differ (hi == lo: lo is a key, and tau).
   uint32_t tau = kKeyPosInf;
   int top = -1;
   if (count([](uint32_t k) { return k == kKeyPosInf; }) < K) {
@@ -642,8 +645,8 @@ __device__ __forceinline__ void list_select(uint32_t* lds, int32_t total, uint32
       tau = hi & ~((2u << top) - 1u);
     }
   }
-  // Below lo the list undercounts but still holds >= 64 >= K keys, so the
-  // `>= K` decisions stand; the exact-K stop waits for a candidate past lo.
+  // Below lo the list undercounts but still holds >= K keys, so the `>= K`
+  // decisions stand; the exact-K stop waits for a candidate past lo.
   for (int bit = top; bit >= 0; --bit) {
     const uint32_t cand = tau | (1u << bit);
     const int32_t n = count([cand](uint32_t k) { return k >= cand; });
@@ -707,8 +710,8 @@ __device__ __forceinline__ void list_select(uint32_t* lds, int32_t total, uint32
 }
 
 // Builds the list from the lane's scores v (block 256*ch + 4*lane + e; -inf
-// past NB) and selects from it; false, with nothing written, when more than
-// kTopkListCap scores are >= lo.
+// past NB) and selects from it; false, with nothing written, when no
+// threshold puts K to kTopkListCap scores at or above it.
 template <int NCH>
 __device__ __forceinline__ bool topk_select_list(const float (&v)[NCH][4], int32_t K, int32_t* orow,
                                                  uint32_t* lds) {
@@ -725,33 +728,72 @@ __device__ __forceinline__ bool topk_select_list(const float (&v)[NCH][4], int32
       imax = b > imax ? b : imax;
       imin = b < imin ? b : imin;
     }
-  const uint32_t lo = wave_min_u32(order_key(__int_as_float(imax >= 0 ? imax : imin)));
-  const float lo_score = key_score(lo);
+  uint32_t lo = wave_min_u32(order_key(__int_as_float(imax >= 0 ? imax : imin)));
   // Scores >= lo go to the list slot by slot ((ch, e) in turn, lanes in
-  // order within a slot); a chunk that would pass the cap ends the attempt.
+  // order within a slot); false when a chunk would pass the cap.
   uint32_t total = 0;  // wave-uniform
+  auto build = [&](float lo_score) -> bool {
+    total = 0;
 #pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) {
-    bool in[4];
-    uint64_t m[4];
-    uint32_t n = 0;
+    for (int ch = 0; ch < NCH; ++ch) {
+      bool in[4];
+      uint64_t m[4];
+      uint32_t n = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      in[e] = v[ch][e] >= lo_score;
-      m[e] = __ballot(in[e]);
-      n += static_cast<uint32_t>(__popcll(m[e]));
-    }
-    if (total + n > kTopkListCap) return false;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (in[e]) {
-        const uint32_t pos = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m[e] >> 32),
-                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m[e]), total));
-        lds[pos] = __float_as_uint(v[ch][e]);
-        lds[kTopkListCap + pos] = static_cast<uint32_t>(256 * ch + 4 * lane + e);
+      for (int e = 0; e < 4; ++e) {
+        in[e] = v[ch][e] >= lo_score;
+        m[e] = __ballot(in[e]);
+        n += static_cast<uint32_t>(__popcll(m[e]));
       }
-      total += static_cast<uint32_t>(__popcll(m[e]));
+      if (total + n > kTopkListCap) return false;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (in[e]) {
+          const uint32_t pos = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m[e] >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m[e]), total));
+          lds[pos] = __float_as_uint(v[ch][e]);
+          lds[kTopkListCap + pos] = static_cast<uint32_t>(256 * ch + 4 * lane + e);
+        }
+        total += static_cast<uint32_t>(__popcll(m[e]));
+      }
     }
+    return true;
+  };
+  if (!build(key_score(lo))) {
+    // More than kTopkListCap scores >= lo: raise lo by the threshold search
+    // over the lane's scores, from the bits lo and the largest finite key
+    // share, to the first candidate with K to kTopkListCap scores at or
+    // above it, and build the list again.  Rows where no such candidate
+    // exists (ties past the cap) take topk_select.
+    uint32_t m = 0;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t k = order_key(v[ch][e]);
+        m = (k < kKeyPosInf && k > m) ? k : m;
+      }
+    const uint32_t hi = wave_max_u32(m);
+    if (hi <= lo) return false;
+    const int top = 31 - __builtin_clz(lo ^ hi);
+    uint32_t tau = hi & ~((2u << top) - 1u);
+    bool found = false;
+    for (int bit = top; bit >= 0 && !found; --bit) {
+      const uint32_t cand = tau | (1u << bit);
+      const float cs = key_score(cand);
+      int32_t n = 0;
+#pragma unroll
+      for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) n += __popcll(__ballot(v[ch][e] >= cs));
+      if (n >= K) {
+        tau = cand;
+        found = n <= kTopkListCap;
+      }
+    }
+    if (!found) return false;
+    lo = tau;
+    if (!build(key_score(lo))) return false;
   }
   __builtin_amdgcn_wave_barrier();
   switch ((total + kWave - 1) / kWave) {
