@@ -497,11 +497,18 @@ __device__ __forceinline__ void topk_select(const uint32_t (&key)[NCH][4], int32
     // A candidate with exactly K keys at or above it decides the selection
     // (keys >= it); the lower bits are then not needed, and the tie rule
     // below takes every key equal to it.
-    for (int bit = searched ? -1 : top; bit >= 0; --bit) {
-      const uint32_t cand = tau | (1u << bit);
-      const int32_t n = count_ge(cand);
-      if (n >= K) tau = cand;
-      if (n == K) break;
+    // Unrolled over the 32 bits (with one chunk, top is 31 at compile time):
+    // each step is its compares and counts, the tau update and one exit
+    // branch, with no loop counter or combined exit condition.
+    if (!searched) {
+#pragma unroll
+      for (int bit = 31; bit >= 0; --bit) {
+        if (bit > top) continue;
+        const uint32_t cand = tau | (1u << bit);
+        const int32_t n = count_ge(cand);
+        if (n >= K) tau = cand;
+        if (n == K) break;
+      }
     }
     need_eq = K - (searched ? n_gt : tau == 0xffffffffu ? 0 : count_ge(tau + 1));
     neg = tau == kKeyNegInf ? need_eq : 0;
@@ -646,12 +653,16 @@ __device__ __forceinline__ void list_select(uint32_t* lds, int32_t total, uint32
     }
   }
   // Below lo the list undercounts but still holds >= K keys, so the `>= K`
-  // decisions stand; the exact-K stop waits for a candidate past lo.
-  for (int bit = top; bit >= 0; --bit) {
-    const uint32_t cand = tau | (1u << bit);
+  // decisions stand.  Exactly K list keys at or above a candidate are the K
+  // largest of the row even below lo (every key >= the K-th largest, ties
+  // included, is >= lo and in the list), so the exact-K stop needs no bound.
+  // The candidate bit is a mask shifted down each step, cleared by the stop:
+  // one scalar loop condition.
+  for (uint32_t b = top < 0 ? 0u : 1u << top; b != 0u;) {
+    const uint32_t cand = tau | b;
     const int32_t n = count([cand](uint32_t k) { return k >= cand; });
     if (n >= K) tau = cand;
-    if (n == K && cand > lo) break;
+    b = n == K ? 0u : b >> 1;
   }
   const int32_t need_eq = K - count([tau](uint32_t k) { return k > tau; });  // >= 0
   const bool neg = tau == kKeyNegInf;  // the tied blocks score -inf: -1 slots, first
@@ -778,8 +789,8 @@ __device__ __forceinline__ bool topk_select_list(const float (&v)[NCH][4], int32
     const int top = 31 - __builtin_clz(lo ^ hi);
     uint32_t tau = hi & ~((2u << top) - 1u);
     bool found = false;
-    for (int bit = top; bit >= 0 && !found; --bit) {
-      const uint32_t cand = tau | (1u << bit);
+    for (uint32_t b = 1u << top; b != 0u;) {
+      const uint32_t cand = tau | b;
       const float cs = key_score(cand);
       int32_t n = 0;
 #pragma unroll
@@ -790,6 +801,7 @@ __device__ __forceinline__ bool topk_select_list(const float (&v)[NCH][4], int32
         tau = cand;
         found = n <= kTopkListCap;
       }
+      b = found ? 0u : b >> 1;
     }
     if (!found) return false;
     lo = tau;
