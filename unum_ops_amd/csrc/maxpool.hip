@@ -205,8 +205,13 @@ __device__ __forceinline__ void load_taps(const PoolArgs& a, const RowCtx& c, in
 __device__ __forceinline__ void pool_taps(const PoolArgs& a, const RowCtx& c, int64_t chunk,
                                           const Taps& tp, float* r) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t n0 = chunk * 256 + 4 * lane;
-  const int64_t avail = c.lim - 4 * n0;
+  // 32-bit arithmetic: block indices, the key length and the token's block
+  // are below 2^31 (int32 sequence offsets), and lim <= 4*NB.
+  const int32_t n0 = static_cast<int32_t>(chunk) * 256 + 4 * lane;
+  const int32_t lim = static_cast<int32_t>(c.lim);
+  const int32_t lk = static_cast<int32_t>(c.lk < INT32_MAX ? c.lk : INT32_MAX);
+  const int32_t ob = static_cast<int32_t>(c.ob);
+  const int32_t avail = lim - 4 * n0;
   float v[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) v[j] = tp.v[j];
@@ -217,15 +222,14 @@ __device__ __forceinline__ void pool_taps(const PoolArgs& a, const RowCtx& c, in
   const float prev = wave_shr1(v[15], tp.below);  // tap 4*n0-1
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int64_t n = n0 + e;
+    const int32_t n = n0 + e;
     const float first = e == 0 ? prev : v[4 * e - 1];
     const float m = fmaxf(fmaxf(first, v[4 * e]),
                           fmaxf(fmaxf(v[4 * e + 1], v[4 * e + 2]), v[4 * e + 3]));
-    const int64_t ws = 4 * n - 1;
-    const int64_t w_lo = ws < 0 ? 0 : ws;
-    const int64_t w_hi = (ws + 5) < c.lk ? (ws + 5) : c.lk;
-    const bool force = n < a.init_blocks || (c.ob >= n && c.ob <= n + a.local_blocks);
-    r[e] = force ? INFINITY : ((w_hi > w_lo) ? m : -INFINITY);
+    // The window 4n-1 .. 4n+3 (from tap 0) holds a tap below lk.
+    const bool any = lk > (n > 0 ? 4 * n - 1 : 0);
+    const bool force = n < a.init_blocks || (ob >= n && ob - n <= a.local_blocks);
+    r[e] = force ? INFINITY : (any ? m : -INFINITY);
   }
 }
 
