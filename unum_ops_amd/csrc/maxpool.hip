@@ -298,6 +298,15 @@ __global__ __launch_bounds__(256) void maxpool_p4_kernel(PoolArgs a) {
 // above a candidate) until it is the K-th largest key or exactly K keys lie
 // at or above it; keys above it are taken, and of the keys equal to it the
 // ones with the lowest block ids, by a running rank.
+// Raw buffer resources: loads past `bytes` read 0 (the range check is per
+// 4-byte word).
+constexpr uint32_t kBufferFlags = 0x00020000;  // gfx9 raw buffer resource word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           static_cast<int>(kBufferFlags));
+}
+
 constexpr int kTopkMaxChunks = 16;  // NB <= 4096 (64 keys per lane)
 constexpr uint32_t kKeyNegInf = 0x007fffffu;  // order_key(-inf)
 constexpr uint32_t kKeyPosInf = 0xff800000u;  // order_key(+inf)

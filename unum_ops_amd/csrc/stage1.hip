@@ -151,6 +151,14 @@ __device__ __forceinline__ float group_sum4(float v) {  // across the 4 lane gro
   return v;
 }
 
+// Raw buffer resources: loads past `bytes` read 0 and stores past it are
+// dropped by the hardware range check.
+constexpr uint32_t kBufferFlags = 0x00020000;  // gfx9 raw buffer resource word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           static_cast<int>(kBufferFlags));
+}
 constexpr int kDropOffset = 0x7fffffff;  // an offset past every range: the store is dropped
 constexpr int kStoreNT = 2;              // buffer store cache policy: non-temporal
 
