@@ -236,9 +236,10 @@ int unum_max_pooling_1d_varlen_topk(const void* input, int64_t input_numel,
  *
  *   pooled   fp32, `rows` rows of num_blocks scores, row r at r * row_stride
  *   topk_idx int32 [rows, topk] contiguous, as unum_max_pooling_1d_varlen_topk
- *            writes it: the topk largest scores, equal scores in ascending
- *            block id, listed in ascending id; -1 for a selected block
- *            scoring -inf and for every slot past num_blocks, -1 entries first.
+ *            writes it: the topk largest scores, equal scores (-0.0 and +0.0
+ *            are one score) in ascending block id, listed in ascending id; -1
+ *            for a selected block scoring -inf and for every slot past
+ *            num_blocks, -1 entries first.
  * 1 <= num_blocks <= 32768 (when rows > 0), row_stride >= num_blocks,
  * rows < 2^31 past 4096 blocks (one workgroup per row there) and < 2^33
  * below; NaN scores are outside the contract.
