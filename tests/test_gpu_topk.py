@@ -249,6 +249,26 @@ def test_topk_blocks_list_selection(kind, NB, dev):
         np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_topk_blocks_random_rows(seed, dev):
+    # Random widths (one chunk to sixteen), slot counts and score mixes: normal
+    # scores, a coarse grid (ties), sprinkled +-inf and -0.0, negative rows.
+    g = torch.Generator().manual_seed(1000 + seed)
+    NB = int(torch.randint(2, 4097, (1,), generator=g))
+    topk = int(torch.randint(1, 66, (1,), generator=g))
+    x = torch.randn(2, 9, NB, generator=g)
+    if seed % 3 == 1:
+        x = torch.floor(x * 3.0) / 3.0
+    if seed % 4 == 2:
+        x = -x.abs() - 0.5
+    r = torch.rand(2, 9, NB, generator=g)
+    x = torch.where(r < 0.03, torch.full_like(x, float("-inf")), x)
+    x = torch.where(r > 0.995, torch.full_like(x, float("inf")), x)
+    x = torch.where((r > 0.4) & (r < 0.41), torch.full_like(x, -0.0), x)
+    got = topk_blocks(x.to(dev), topk)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle_topk(x, topk))
+
+
 @pytest.mark.parametrize("NB", [200, 2112, 5000])
 def test_topk_blocks_signed_zeros(NB, dev):
     # One chunk, the list selection, and one workgroup a row: -0.0 ranks as
