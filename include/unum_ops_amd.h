@@ -211,9 +211,10 @@ int unum_max_pooling_1d_varlen(const void* input, int64_t input_numel, int32_t d
  * top-k ids, sorted ascending), with a deterministic tie-break.
  *
  *   topk_idx int32 [H, Tq, topk]: per (h, t), the topk blocks with the largest
- *            pooled scores, equal scores taken in ascending block id, listed in
- *            ascending id; a selected block scoring -inf and every slot past
- *            num_blocks is -1, and the -1 entries come first.
+ *            pooled scores, equal scores (-0.0 and +0.0 are one score) taken
+ *            in ascending block id, listed in ascending id; a selected block
+ *            scoring -inf and every slot past num_blocks is -1, and the -1
+ *            entries come first.  NaN inputs are outside the contract.
  *   pooled   optional [H, Tq, num_blocks] fp32 (NULL: not written); when given
  *            it must be 16-byte aligned with num_blocks % 4 == 0.
  * Other arguments as unum_max_pooling_1d_varlen.  num_blocks <= 4096,
